@@ -1,0 +1,124 @@
+/* sffft.h - C ABI of the MI355X fused causal long-convolution library (libsffft.so).
+ *
+ *   y[b,h,n] = sum_{m<=n} u[b,h,m] * k[h,n-m],  n < L,  L a power of two in [128, 16384]
+ *
+ * The reference has no library: its interface is two kernel launches inside
+ * src/sffft.cu. Each entry point below names the reference code it replaces.
+ *
+ * Conventions
+ *  - All pointers are device pointers (hipMalloc'd) unless stated otherwise.
+ *    u and y are [B][H][L] row-major; k is [H][L]; rows must be 16-byte aligned.
+ *  - `stream` is a hipStream_t (NULL = default stream). Calls are asynchronous on
+ *    that stream, reentrant, and allocate no memory, except that the first call on a
+ *    device uploads an immutable 57,344-byte DFT coefficient table (kept for the
+ *    life of the process).
+ *  - Every function returns SFFFT_OK (0) or a positive error code; nothing exits.
+ */
+#ifndef SFFFT_H
+#define SFFFT_H
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define SFFFT_OK 0
+#define SFFFT_EINVAL 1      /* invalid argument (sizes, plan, null pointer, misalignment) */
+#define SFFFT_ENOPLAN 2     /* the plan is valid but was not compiled into this library */
+#define SFFFT_EHIP 3        /* the HIP runtime reported an error */
+#define SFFFT_ENOTFOUND 4   /* no candidate/plan matches the request */
+
+/* A transform plan: N = 2L = r0*r1*r2 (r2 = 1 for two-stage plans), radices in
+ * {16,32,64}. Mirrors Plan<R0,R1,R2> and the W template argument of fftconv
+ * (src/sffft.cu:92-104, 243-245, 507-513).
+ *   waves : wavefronts (64 lanes) per workgroup
+ *   acc   : 0 = fp32 accumulation, 1 = fp16 accumulation ("fp16acc" methods)
+ *   cached: 1 = DFT matrices from the coefficient table ("kernel_cached"),
+ *           0 = computed in the kernel ("kernel_legacy")  (src/sffft.cu:253-265)
+ *   seqs  : sequences per workgroup: 1, or 2 (two batch rows of one channel packed
+ *           as the real and imaginary parts of one complex transform; B must be even)
+ */
+typedef struct sffft_plan {
+  int r0, r1, r2;
+  int waves;
+  int acc;
+  int cached;
+  int seqs;
+} sffft_plan;
+
+/* Plan validity: SFFFT_OK, SFFFT_EINVAL (bad radices/product/LDS), SFFFT_ENOPLAN.
+ * Replaces the host check `if (P::L != L)` (src/sffft.cu:383). */
+int sffft_plan_check(int L, const sffft_plan* plan);
+
+/* LDS bytes per workgroup (Plan::smem<W,TAcc>(), src/sffft.cu:103). 0 if invalid. */
+size_t sffft_plan_lds_bytes(int L, const sffft_plan* plan);
+
+/* Workgroups of this plan resident per CU (cudaOccupancyMaxActiveBlocksPerMultiprocessor,
+ * src/sffft.cu:388). Requires a HIP device. */
+int sffft_plan_occupancy(int L, const sffft_plan* plan, int* blocks_per_cu);
+
+/* The plan registry used by the driver and the selector: the i-th compiled plan
+ * for length L (acc = 0, cached = 1 are filled in; callers vary them). Writes the
+ * plan name ("64x32") into name. Returns SFFFT_ENOTFOUND past the end.
+ * Replaces the RUN(...) plan table (src/sffft.cu:506-513). */
+int sffft_plan_count(int L);
+int sffft_plan_get(int L, int index, sffft_plan* plan, char* name, size_t name_len);
+
+/* Bytes of the kernel-order filter spectrum: H * 2L * 8 (complex64). */
+size_t sffft_spectrum_bytes(int H, int L);
+
+/* Filter spectrum in the fused kernel's order, from the real filter k [H][L] fp32.
+ * `work` must hold sffft_spectrum_bytes(H, L) bytes (scratch, clobbered).
+ * Replaces: zero-pad + cufftExecC2C(FORWARD) + permuteK (src/sffft.cu:342-344,365,384,283-288).
+ * Arithmetic: fp64 accumulation and twiddles, fp32 storage between the stages. */
+int sffft_spectrum(const float* k, int H, int L, const sffft_plan* plan, void* kf, void* work, void* stream);
+
+/* Same, from an unnormalised natural-order spectrum kc [H][2L] complex64
+ * (kc[h][f] = sum_n k[h][n] exp(-2 pi i f n / 2L), e.g. from hipFFT C2C).
+ * Replaces permuteK (src/sffft.cu:283-288). kc and kf must not overlap. */
+int sffft_spectrum_from_natural(const void* kc, int H, int L, const sffft_plan* plan, void* kf, void* stream);
+
+/* The fused convolution, one launch: grid = H*B/seqs workgroups of 64*waves lanes.
+ * Replaces fftconv<P,W,float|bf16,TAcc,CACHED><<<B*H, 32*W, smem>>> (src/sffft.cu:243-280,389-390).
+ * kf must come from sffft_spectrum* with the same L and the same r0/r1/r2. */
+int sffft_conv_f32(const float* u, const void* kf, float* y, int B, int H, int L, const sffft_plan* plan,
+                   void* stream);
+/* bf16 I/O: u and y hold bf16 bit patterns; y is rounded to nearest even. */
+int sffft_conv_bf16(const uint16_t* u, const void* kf, uint16_t* y, int B, int H, int L,
+                    const sffft_plan* plan, void* stream);
+
+/* fp32 -> bf16 (round to nearest even) on the device. Replaces tobf16 (src/sffft.cu:306). */
+int sffft_to_bf16(const float* x, uint16_t* y, size_t n, void* stream);
+
+/* Copies the device DFT coefficient table (57,344 bytes) to host memory `out`
+ * (for tests). Returns SFFFT_EINVAL if out_len is too small. */
+int sffft_dft_table(void* out, size_t out_len);
+
+/* Host-side selector (src/selection.h:8-29). A candidate is (method, io, config, ms,
+ * rel_err); io is "fp32" or "bf16". Returns the index of the fastest candidate whose io
+ * matches (io "any" matches both), with finite ms > 0 and finite 0 <= rel_err <=
+ * max_error, ties on ms going to the lower rel_err; -1 if none or if max_error is not
+ * positive and finite or io is unknown. */
+typedef struct sffft_candidate {
+  const char* method;
+  const char* io;
+  const char* config;
+  double ms;
+  double rel_err;
+} sffft_candidate;
+int sffft_select_candidate(const sffft_candidate* candidates, int n, double max_error, const char* io);
+
+/* sqrt(squared_error / squared_reference); a zero reference gives 0 for a zero
+ * error and +inf otherwise (src/selection.h:26-29). */
+double sffft_relative_l2(double squared_error, double squared_reference);
+
+const char* sffft_strerror(int code);
+
+/* Text of the last HIP error recorded by a call on this thread ("" if none). */
+const char* sffft_last_error(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* SFFFT_H */

@@ -1,0 +1,249 @@
+"""MI355X fused causal long convolution: Python binding of libsffft.so.
+
+y[b,h,n] = sum_{m<=n} u[b,h,m] * k[h,n-m] in one fused HIP launch per batch.
+
+This module is a thin ctypes layer over the C ABI declared in include/sffft.h
+(the drop-in boundary). torch supplies device memory and the current stream;
+every computation runs in libsffft.so. There is no fallback: if the library is
+missing or a call fails, an exception is raised.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from typing import List, Optional, Tuple
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libsffft.so")
+CLI_PATH = os.path.join(_HERE, "sffft")
+ROCFFT_LIB_PATH = os.path.join(_HERE, "libsffft_rocfft.so")
+HEADER_PATH = os.path.join(os.path.dirname(_HERE), "include", "sffft.h")
+
+SFFFT_OK, SFFFT_EINVAL, SFFFT_ENOPLAN, SFFFT_EHIP, SFFFT_ENOTFOUND = 0, 1, 2, 3, 4
+LENGTHS = (128, 256, 512, 1024, 2048, 4096, 8192, 16384)
+
+
+class Plan(ctypes.Structure):
+    """sffft_plan: N = 2L = r0*r1*r2 (r2 = 1 for two-stage plans)."""
+
+    _fields_ = [
+        ("r0", ctypes.c_int),
+        ("r1", ctypes.c_int),
+        ("r2", ctypes.c_int),
+        ("waves", ctypes.c_int),
+        ("acc", ctypes.c_int),
+        ("cached", ctypes.c_int),
+        ("seqs", ctypes.c_int),
+    ]
+
+    def name(self) -> str:
+        return f"{self.r0}x{self.r1}" + (f"x{self.r2}" if self.r2 > 1 else "")
+
+    def replace(self, **kw) -> "Plan":
+        d = {f: getattr(self, f) for f, _ in self._fields_}
+        d.update(kw)
+        return Plan(**d)
+
+    def __repr__(self) -> str:
+        return (f"Plan({self.name()}, waves={self.waves}, acc={self.acc}, cached={self.cached}, "
+                f"seqs={self.seqs})")
+
+
+class Candidate(ctypes.Structure):
+    _fields_ = [
+        ("method", ctypes.c_char_p),
+        ("io", ctypes.c_char_p),
+        ("config", ctypes.c_char_p),
+        ("ms", ctypes.c_double),
+        ("rel_err", ctypes.c_double),
+    ]
+
+
+class SffftError(RuntimeError):
+    def __init__(self, code: int, what: str):
+        detail = lib().sffft_last_error().decode() if code == SFFFT_EHIP else ""
+        super().__init__(f"{what}: {strerror(code)} (code {code}) {detail}".rstrip())
+        self.code = code
+
+
+_lib = None
+
+
+def lib() -> ctypes.CDLL:
+    """Loads libsffft.so (built in-tree by `make -C sffft_amd`)."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(f"{LIB_PATH} is missing: build it with `make -C sffft_amd` "
+                               "(or __graft_entry__.build())")
+        # PyTorch ships its own HIP runtime under the same soname as /opt/rocm's.
+        # Import it first so libsffft.so binds to the runtime torch uses: two HIP
+        # runtimes in one process do not share devices, memory or streams.
+        try:
+            import torch  # noqa: F401
+        except ImportError:
+            pass
+        L = ctypes.CDLL(LIB_PATH)
+        P = ctypes.POINTER(Plan)
+        vp, ci, sz = ctypes.c_void_p, ctypes.c_int, ctypes.c_size_t
+        sigs = {
+            "sffft_plan_check": (ci, [ci, P]),
+            "sffft_plan_lds_bytes": (sz, [ci, P]),
+            "sffft_plan_occupancy": (ci, [ci, P, ctypes.POINTER(ci)]),
+            "sffft_plan_count": (ci, [ci]),
+            "sffft_plan_get": (ci, [ci, ci, P, ctypes.c_char_p, sz]),
+            "sffft_spectrum_bytes": (sz, [ci, ci]),
+            "sffft_spectrum": (ci, [vp, ci, ci, P, vp, vp, vp]),
+            "sffft_spectrum_from_natural": (ci, [vp, ci, ci, P, vp, vp]),
+            "sffft_conv_f32": (ci, [vp, vp, vp, ci, ci, ci, P, vp]),
+            "sffft_conv_bf16": (ci, [vp, vp, vp, ci, ci, ci, P, vp]),
+            "sffft_to_bf16": (ci, [vp, vp, sz, vp]),
+            "sffft_dft_table": (ci, [vp, sz]),
+            "sffft_select_candidate": (ci, [ctypes.POINTER(Candidate), ci, ctypes.c_double, ctypes.c_char_p]),
+            "sffft_relative_l2": (ctypes.c_double, [ctypes.c_double, ctypes.c_double]),
+            "sffft_strerror": (ctypes.c_char_p, [ci]),
+            "sffft_last_error": (ctypes.c_char_p, []),
+        }
+        for name, (res, args) in sigs.items():
+            f = getattr(L, name)
+            f.restype, f.argtypes = res, args
+        _lib = L
+    return _lib
+
+
+def strerror(code: int) -> str:
+    return lib().sffft_strerror(code).decode()
+
+
+def _check(code: int, what: str) -> None:
+    if code != SFFFT_OK:
+        raise SffftError(code, what)
+
+
+def plans(L: int) -> List[Plan]:
+    """Compiled plans for length L (acc=0, cached=1); vary acc/cached/seqs as needed."""
+    out = []
+    for i in range(lib().sffft_plan_count(L)):
+        p = Plan()
+        _check(lib().sffft_plan_get(L, i, ctypes.byref(p), None, 0), "sffft_plan_get")
+        out.append(p)
+    return out
+
+
+def make_plan(spec: str, waves: int, acc: int = 0, cached: int = 1, seqs: int = 1) -> Plan:
+    r = [int(x) for x in spec.split("x")]
+    r += [1] * (3 - len(r))
+    return Plan(r[0], r[1], r[2], waves, acc, cached, seqs)
+
+
+def plan_check(L: int, plan: Plan) -> int:
+    return lib().sffft_plan_check(L, ctypes.byref(plan))
+
+
+def lds_bytes(L: int, plan: Plan) -> int:
+    return lib().sffft_plan_lds_bytes(L, ctypes.byref(plan))
+
+
+def occupancy(L: int, plan: Plan) -> int:
+    n = ctypes.c_int(0)
+    _check(lib().sffft_plan_occupancy(L, ctypes.byref(plan), ctypes.byref(n)), "sffft_plan_occupancy")
+    return n.value
+
+
+def select_candidate(cands: List[Tuple[str, str, str, float, float]], max_error: float, io: str) -> int:
+    arr = (Candidate * max(1, len(cands)))()
+    keep = []
+    for i, (m, o, c, ms, err) in enumerate(cands):
+        b = [m.encode(), o.encode(), c.encode()]
+        keep.append(b)
+        arr[i] = Candidate(b[0], b[1], b[2], ms, err)
+    return lib().sffft_select_candidate(arr, len(cands), max_error, io.encode())
+
+
+def relative_l2(squared_error: float, squared_reference: float) -> float:
+    return lib().sffft_relative_l2(squared_error, squared_reference)
+
+
+# ---- torch-facing helpers (device memory and streams come from torch) ----------
+def _stream():
+    import torch
+
+    return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+
+def _ptr(t) -> ctypes.c_void_p:
+    return ctypes.c_void_p(t.data_ptr())
+
+
+def spectrum(k, L: int, plan: Plan, work=None):
+    """Kernel-order filter spectrum [H, 2L] complex64 from the real filter k [H, L] (fp32, cuda)."""
+    import torch
+
+    assert k.is_cuda and k.dtype == torch.float32 and k.dim() == 2 and k.shape[1] == L
+    k = k.contiguous()
+    H = k.shape[0]
+    kf = torch.empty((H, 2 * L), dtype=torch.complex64, device=k.device)
+    if work is None:
+        work = torch.empty_like(kf)
+    _check(lib().sffft_spectrum(_ptr(k), H, L, ctypes.byref(plan), _ptr(kf), _ptr(work), _stream()),
+           "sffft_spectrum")
+    return kf
+
+
+def spectrum_from_natural(kc, L: int, plan: Plan):
+    """Kernel-order spectrum from the unnormalised natural-order spectrum kc [H, 2L] complex64."""
+    import torch
+
+    assert kc.is_cuda and kc.dtype == torch.complex64 and kc.shape[1] == 2 * L
+    kc = kc.contiguous()
+    kf = torch.empty_like(kc)
+    _check(lib().sffft_spectrum_from_natural(_ptr(kc), kc.shape[0], L, ctypes.byref(plan), _ptr(kf), _stream()),
+           "sffft_spectrum_from_natural")
+    return kf
+
+
+def conv(u, kf, plan: Plan, out=None):
+    """y = causal_conv(u, k) for u [B, H, L] fp32 or bf16 (cuda), kf from spectrum()."""
+    import torch
+
+    assert u.is_cuda and u.dim() == 3
+    u = u.contiguous()
+    B, H, L = u.shape
+    y = torch.empty_like(u) if out is None else out
+    if u.dtype == torch.float32:
+        fn = lib().sffft_conv_f32
+    elif u.dtype == torch.bfloat16:
+        fn = lib().sffft_conv_bf16
+    else:
+        raise TypeError(f"unsupported dtype {u.dtype}")
+    _check(fn(_ptr(u), _ptr(kf), _ptr(y), B, H, L, ctypes.byref(plan), _stream()), "sffft_conv")
+    return y
+
+
+def to_bf16(x):
+    import torch
+
+    y = torch.empty(x.shape, dtype=torch.bfloat16, device=x.device)
+    _check(lib().sffft_to_bf16(_ptr(x.contiguous()), _ptr(y), x.numel(), _stream()), "sffft_to_bf16")
+    return y
+
+
+def dft_table():
+    import numpy as np
+
+    buf = (ctypes.c_uint16 * (57344 // 2))()
+    _check(lib().sffft_dft_table(buf, 57344), "sffft_dft_table")
+    return np.frombuffer(buf, dtype=np.uint16).copy()
+
+
+def loaded_library_paths() -> List[str]:
+    """Shared objects of this package mapped into the process (for load checks)."""
+    out = []
+    try:
+        with open("/proc/self/maps") as f:
+            for line in f:
+                if _HERE in line and line.rstrip().endswith(".so"):
+                    out.append(line.split()[-1])
+    except OSError:
+        pass
+    return sorted(set(out))

@@ -1,0 +1,411 @@
+// C ABI of libsffft.so: plan checks, the DFT coefficient table, filter-spectrum
+// preparation, the fused convolution launch and the host-side selector.
+#include <hip/hip_runtime.h>
+
+#include <climits>
+#include <cmath>
+#include <cstring>
+#include <limits>
+#include <mutex>
+#include <vector>
+
+#include "../../include/sffft.h"
+#include "fftconv.hpp"
+#include "registry.hpp"
+
+namespace sffft {
+namespace {
+
+thread_local char g_last_error[256] = "";
+
+// Records the HIP error of the last failing call on this thread.
+int hip_status(hipError_t err, const char* what) {
+  if (err == hipSuccess) return SFFFT_OK;
+  snprintf(g_last_error, sizeof(g_last_error), "%s: %s (%d)", what, hipGetErrorString(err), (int)err);
+  return SFFFT_EHIP;
+}
+
+bool valid_radix(int r) { return r == 16 || r == 32 || r == 64; }
+bool valid_length(int L) { return L >= 128 && L <= 16384 && (L & (L - 1)) == 0; }
+bool valid_waves(int w) { return w == 1 || w == 2 || w == 4 || w == 8 || w == 16; }
+
+// Same formula as Plan<>::LDS_BYTES, for plans that are not compiled.
+size_t lds_bytes_rt(int r0, int r1, int r2) {
+  const int S = r2 > 1 ? 3 : 2, N = r0 * r1 * r2, M = N / r0;
+  const int PA = r1 + LDS_PAD, PB = r0 + LDS_PAD, PC = r2 + LDS_PAD;
+  const int ROW = S == 3 ? cmax(r2 * PA, r1 * PC) : 0;
+  const int P0 = S == 3 ? cmax(r0 * ROW, M * PB) : cmax(r0 * PA, r1 * PB);
+  return (size_t)(((P0 + 63) & ~63) * 4);
+}
+
+const Entry* entries_for(int L, int* n) {
+  switch (L) {
+    case 128: return entries_L128(n);
+    case 256: return entries_L256(n);
+    case 512: return entries_L512(n);
+    case 1024: return entries_L1024(n);
+    case 2048: return entries_L2048(n);
+    case 4096: return entries_L4096(n);
+    case 8192: return entries_L8192(n);
+    case 16384: return entries_L16384(n);
+    default: *n = 0; return nullptr;
+  }
+}
+
+int check_shape(int L, const sffft_plan* p) {
+  if (!p || !valid_length(L)) return SFFFT_EINVAL;
+  if (!valid_radix(p->r0) || !valid_radix(p->r1) || !(p->r2 == 1 || valid_radix(p->r2))) return SFFFT_EINVAL;
+  if ((long long)p->r0 * p->r1 * p->r2 != 2LL * L) return SFFFT_EINVAL;
+  if (!valid_waves(p->waves) || (p->acc != 0 && p->acc != 1) || (p->cached != 0 && p->cached != 1) ||
+      (p->seqs != 1 && p->seqs != 2))
+    return SFFFT_EINVAL;
+  if (p->r2 > 1 && p->r0 % p->waves) return SFFFT_EINVAL;
+  if (lds_bytes_rt(p->r0, p->r1, p->r2) > 163840) return SFFFT_EINVAL;
+  return SFFFT_OK;
+}
+
+const Entry* find_entry(int L, const sffft_plan* p) {
+  int n = 0;
+  const Entry* e = entries_for(L, &n);
+  for (int i = 0; i < n; i++)
+    if (e[i].r0 == p->r0 && e[i].r1 == p->r1 && e[i].r2 == p->r2 && e[i].waves == p->waves && e[i].seqs == p->seqs)
+      return &e[i];
+  return nullptr;
+}
+
+// ---- DFT coefficient table (the "cached" DFT matrices, src/sffft.cu:349-362) ----
+// Entries are __float2half((float)cos(angle)) / (float)-sin(angle) of the exact
+// angle 2*pi*(e mod R)/R, as in the reference table, arranged as MFMA fragments.
+void build_table(std::vector<_Float16>& t) {
+  t.assign((size_t)FTAB_H8 * 8, (_Float16)0.f);
+  const double two_pi = 6.283185307179586476925286766559;
+  auto cs = [&](int e, int R, float* c, float* s) {
+    const double a = two_pi * (double)(e % R) / (double)R;
+    *c = (float)std::cos(a);
+    *s = (float)std::sin(a);
+  };
+  for (int R : {16, 32, 64}) {
+    const int T = R / 16;
+    for (int a = 0; a < T; a++)
+      for (int b = 0; b < T; b++)
+        for (int kind = 0; kind < 2; kind++)
+          for (int lane = 0; lane < 64; lane++) {
+            const int r = lane & 15, g = lane >> 4;
+            _Float16* f = &t[((size_t)cf_off(R) + ((a * T + b) * 2 + kind) * 64 + lane) * 8];
+            for (int v = 0; v < 4; v++) {
+              float c, s;
+              cs((16 * a + r) * (16 * b + 4 * g + v), R, &c, &s);
+              f[v] = (_Float16)(kind == 0 ? c : -s);
+              f[4 + v] = (_Float16)(kind == 0 ? s : c);
+            }
+          }
+    for (int nt = 0; nt < T; nt++)
+      for (int kind = 0; kind < 2; kind++)
+        for (int lane = 0; lane < 64; lane++) {
+          const int c16 = lane & 15, g = lane >> 4;
+          _Float16* f = &t[((size_t)ri_off(R) + (nt * 2 + kind) * 64 + lane) * 8];
+          for (int j = 0; j < 8; j++) {
+            const int n0 = j < 4 ? 4 * g + j : 16 + 4 * g + (j - 4);
+            float c, s;
+            cs(n0 * (16 * nt + c16), R, &c, &s);
+            f[j] = n0 >= R / 2 ? (_Float16)0.f : (_Float16)(kind == 0 ? c : -s);
+          }
+        }
+  }
+}
+
+std::mutex g_table_mu;
+void* g_table[256];
+
+int device_table(const void** out) {
+  int dev = 0;
+  hipError_t err = hipGetDevice(&dev);
+  if (err != hipSuccess) return hip_status(err, "hipGetDevice");
+  if (dev < 0 || dev >= 256) return SFFFT_EINVAL;
+  std::lock_guard<std::mutex> lock(g_table_mu);
+  if (!g_table[dev]) {
+    std::vector<_Float16> host;
+    build_table(host);
+    void* d = nullptr;
+    if ((err = hipMalloc(&d, host.size() * sizeof(_Float16))) != hipSuccess) return hip_status(err, "hipMalloc");
+    if ((err = hipMemcpy(d, host.data(), host.size() * sizeof(_Float16), hipMemcpyHostToDevice)) != hipSuccess) {
+      (void)hipFree(d);
+      return hip_status(err, "hipMemcpy");
+    }
+    g_table[dev] = d;
+  }
+  *out = g_table[dev];
+  return SFFFT_OK;
+}
+
+// ---- filter spectrum ----------------------------------------------------------
+// Runtime form of kernel_order_digits<P>.
+__device__ inline void kernel_order_digits_rt(int idx, int r0, int r1, int r2, int& k0, int& k1, int& k2) {
+  const int v = idx & 3, lane = (idx >> 2) & 63, rest = idx >> 8;
+  const int c = lane & 15, g = lane >> 4;
+  if (r2 == 1) {
+    const int T1 = r1 / 16, mt = rest % T1, s = rest / T1;
+    k0 = 16 * s + c;
+    k1 = 16 * mt + 4 * g + v;
+    k2 = 0;
+  } else {
+    const int T1 = r1 / 16, T2 = r2 / 16;
+    const int mt = rest % T2, t1 = (rest / T2) % T1;
+    k0 = rest / (T2 * T1);
+    k1 = 16 * t1 + c;
+    k2 = 16 * mt + 4 * g + v;
+  }
+}
+
+// One in-place decimation-in-frequency stage over digit J (Appendix-A order of the
+// reference: after all stages position p = d0*(R1 R2) + d1*R2 + d2 holds
+// DFT_N(pad(k))[d0 + R0 d1 + R0 R1 d2]). One thread per line of R_J points; fp64
+// arithmetic, fp32 storage. Stage 0 reads the real filter rows zero-padded to N.
+__global__ void spectrum_stage_kernel(const float* __restrict__ k, float2* work, int H, int L, int r0, int r1,
+                                      int r2, int J) {
+  __shared__ double wc[64], ws[64];
+  const int N = r0 * r1 * r2, S = r2 > 1 ? 3 : 2;
+  const int R = J == 0 ? r0 : J == 1 ? r1 : r2;
+  const int sJ = J == 0 ? r1 * r2 : J == 1 ? r2 : 1;
+  for (int i = threadIdx.x; i < R; i += blockDim.x) {
+    double s, c;
+    sincospi(2.0 * (double)i / (double)R, &s, &c);
+    wc[i] = c;
+    ws[i] = s;
+  }
+  __syncthreads();
+  const int lines = N / R;
+  const size_t gid = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (gid >= (size_t)H * lines) return;
+  const int h = (int)(gid / lines), l = (int)(gid % lines);
+  const int inner = l % sJ, outer = l / sJ;
+  const int base = outer * R * sJ + inner;
+  float2* row = work + (size_t)h * N;
+  float2 x[64];
+  for (int t = 0; t < R; t++) {
+    const int p = base + t * sJ;
+    if (J == 0)
+      x[t] = make_float2(p < L ? k[(size_t)h * L + p] : 0.f, 0.f);
+    else
+      x[t] = row[p];
+  }
+  const int mul = N / (R * sJ);
+  for (int kk = 0; kk < R; kk++) {
+    double ar = 0.0, ai = 0.0;
+    for (int t = 0; t < R; t++) {
+      const int e = (t * kk) % R;
+      const double c = wc[e], s = ws[e];  // exp(-i theta) = c - i s
+      ar += (double)x[t].x * c + (double)x[t].y * s;
+      ai += (double)x[t].y * c - (double)x[t].x * s;
+    }
+    if (J != S - 1) {
+      const int e = (mul * inner * kk) % N;
+      double s, c;
+      sincospi(2.0 * (double)e / (double)N, &s, &c);
+      const double tr = ar * c + ai * s, ti = ai * c - ar * s;
+      ar = tr;
+      ai = ti;
+    }
+    row[base + kk * sJ] = make_float2((float)ar, (float)ai);
+  }
+}
+
+// Gather into the fused kernel's order, folding in 1/sqrt(R_last) of the last
+// forward stage. src is p-order (natural == 0) or natural frequency order.
+__global__ void spectrum_permute_kernel(const float2* __restrict__ src, float2* __restrict__ kf, int H, int r0,
+                                        int r1, int r2, int natural, float scale) {
+  const int N = r0 * r1 * r2;
+  const size_t gid = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (gid >= (size_t)H * N) return;
+  const int h = (int)(gid / N), idx = (int)(gid % N);
+  int k0, k1, k2;
+  kernel_order_digits_rt(idx, r0, r1, r2, k0, k1, k2);
+  const int s = natural ? k0 + r0 * k1 + r0 * r1 * k2 : k0 * (r1 * r2) + k1 * r2 + k2;
+  const float2 v = src[(size_t)h * N + s];
+  kf[gid] = make_float2(v.x * scale, v.y * scale);
+}
+
+__global__ void to_bf16_kernel(const float* __restrict__ x, uint16_t* __restrict__ y, size_t n) {
+  const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) y[i] = f32_to_bf16(x[i]);
+}
+
+float last_stage_scale(const sffft_plan* p) {
+  const int R = p->r2 > 1 ? p->r2 : p->r1;
+  return (float)(1.0 / std::sqrt((double)R));
+}
+
+bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+template <int IO>
+int conv(const void* u, const void* kf, void* y, int B, int H, int L, const sffft_plan* p, void* stream) {
+  if (!u || !kf || !y || B < 1 || H < 1 || (long long)B * H > INT_MAX) return SFFFT_EINVAL;
+  int rc = check_shape(L, p);
+  if (rc) return rc;
+  if (B % p->seqs) return SFFFT_EINVAL;
+  if (!aligned16(u) || !aligned16(y) || !aligned16(kf)) return SFFFT_EINVAL;
+  const Entry* e = find_entry(L, p);
+  if (!e) return SFFFT_ENOPLAN;
+  const void* table = nullptr;
+  if ((rc = device_table(&table))) return rc;
+  return hip_status(e->launch[IO][p->cached](u, kf, y, B, H, table, p->acc, (hipStream_t)stream),
+                    "fused convolution launch");
+}
+
+}  // namespace
+}  // namespace sffft
+
+using namespace sffft;
+
+extern "C" {
+
+int sffft_plan_check(int L, const sffft_plan* plan) {
+  const int rc = check_shape(L, plan);
+  if (rc) return rc;
+  return find_entry(L, plan) ? SFFFT_OK : SFFFT_ENOPLAN;
+}
+
+size_t sffft_plan_lds_bytes(int L, const sffft_plan* plan) {
+  if (check_shape(L, plan)) return 0;
+  return lds_bytes_rt(plan->r0, plan->r1, plan->r2);
+}
+
+int sffft_plan_occupancy(int L, const sffft_plan* plan, int* blocks_per_cu) {
+  if (!blocks_per_cu) return SFFFT_EINVAL;
+  const int rc = sffft_plan_check(L, plan);
+  if (rc) return rc;
+  const Entry* e = find_entry(L, plan);
+  int n = 0;
+  const int st = hip_status(
+      hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, e->func[0][plan->cached], 64 * plan->waves, 0),
+      "hipOccupancyMaxActiveBlocksPerMultiprocessor");
+  if (st) return st;
+  *blocks_per_cu = n;
+  return SFFFT_OK;
+}
+
+int sffft_plan_count(int L) {
+  int n = 0;
+  entries_for(L, &n);
+  return n;
+}
+
+int sffft_plan_get(int L, int index, sffft_plan* plan, char* name, size_t name_len) {
+  int n = 0;
+  const Entry* e = entries_for(L, &n);
+  if (index < 0 || index >= n) return SFFFT_ENOTFOUND;
+  if (plan) {
+    plan->r0 = e[index].r0;
+    plan->r1 = e[index].r1;
+    plan->r2 = e[index].r2;
+    plan->waves = e[index].waves;
+    plan->seqs = e[index].seqs;
+    plan->acc = 0;
+    plan->cached = 1;
+  }
+  if (name && name_len) {
+    if (e[index].r2 > 1)
+      snprintf(name, name_len, "%dx%dx%d", e[index].r0, e[index].r1, e[index].r2);
+    else
+      snprintf(name, name_len, "%dx%d", e[index].r0, e[index].r1);
+  }
+  return SFFFT_OK;
+}
+
+size_t sffft_spectrum_bytes(int H, int L) {
+  if (H < 1 || !valid_length(L)) return 0;
+  return (size_t)H * 2 * L * 8;
+}
+
+int sffft_spectrum(const float* k, int H, int L, const sffft_plan* plan, void* kf, void* work, void* stream) {
+  if (!k || !kf || !work || H < 1 || kf == work) return SFFFT_EINVAL;
+  const int rc = check_shape(L, plan);
+  if (rc) return rc;
+  const int N = 2 * L, S = plan->r2 > 1 ? 3 : 2;
+  hipStream_t s = (hipStream_t)stream;
+  float2* w = static_cast<float2*>(work);
+  for (int J = 0; J < S; J++) {
+    const int R = J == 0 ? plan->r0 : J == 1 ? plan->r1 : plan->r2;
+    const size_t threads = (size_t)H * (N / R);
+    hipLaunchKernelGGL(spectrum_stage_kernel, dim3((unsigned)((threads + 127) / 128)), dim3(128), 0, s, k, w, H, L,
+                       plan->r0, plan->r1, plan->r2, J);
+    const int st = hip_status(hipGetLastError(), "spectrum stage launch");
+    if (st) return st;
+  }
+  const size_t total = (size_t)H * N;
+  hipLaunchKernelGGL(spectrum_permute_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s,
+                     (const float2*)w, static_cast<float2*>(kf), H, plan->r0, plan->r1, plan->r2, 0,
+                     last_stage_scale(plan));
+  return hip_status(hipGetLastError(), "spectrum permute launch");
+}
+
+int sffft_spectrum_from_natural(const void* kc, int H, int L, const sffft_plan* plan, void* kf, void* stream) {
+  if (!kc || !kf || H < 1 || kc == kf) return SFFFT_EINVAL;
+  const int rc = check_shape(L, plan);
+  if (rc) return rc;
+  const size_t total = (size_t)H * 2 * L;
+  hipLaunchKernelGGL(spectrum_permute_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0,
+                     (hipStream_t)stream, static_cast<const float2*>(kc), static_cast<float2*>(kf), H, plan->r0,
+                     plan->r1, plan->r2, 1, last_stage_scale(plan));
+  return hip_status(hipGetLastError(), "spectrum permute launch");
+}
+
+int sffft_conv_f32(const float* u, const void* kf, float* y, int B, int H, int L, const sffft_plan* plan,
+                   void* stream) {
+  return conv<0>(u, kf, y, B, H, L, plan, stream);
+}
+
+int sffft_conv_bf16(const uint16_t* u, const void* kf, uint16_t* y, int B, int H, int L, const sffft_plan* plan,
+                    void* stream) {
+  return conv<1>(u, kf, y, B, H, L, plan, stream);
+}
+
+int sffft_to_bf16(const float* x, uint16_t* y, size_t n, void* stream) {
+  if (!x || !y) return SFFFT_EINVAL;
+  if (!n) return SFFFT_OK;
+  hipLaunchKernelGGL(to_bf16_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, (hipStream_t)stream, x, y, n);
+  return hip_status(hipGetLastError(), "to_bf16 launch");
+}
+
+int sffft_dft_table(void* out, size_t out_len) {
+  const size_t bytes = (size_t)FTAB_H8 * 16;
+  if (!out || out_len < bytes) return SFFFT_EINVAL;
+  const void* table = nullptr;
+  const int rc = device_table(&table);
+  if (rc) return rc;
+  return hip_status(hipMemcpy(out, table, bytes, hipMemcpyDeviceToHost), "hipMemcpy");
+}
+
+int sffft_select_candidate(const sffft_candidate* c, int n, double max_error, const char* io) {
+  if (!std::isfinite(max_error) || max_error <= 0 || !io) return -1;
+  if (std::strcmp(io, "fp32") && std::strcmp(io, "bf16") && std::strcmp(io, "any")) return -1;
+  int best = -1;
+  for (int i = 0; i < n; i++) {
+    if (!c || !c[i].io) continue;
+    if (std::strcmp(io, "any") && std::strcmp(io, c[i].io)) continue;
+    const double ms = c[i].ms, err = c[i].rel_err;
+    if (!std::isfinite(ms) || ms <= 0 || !std::isfinite(err) || err < 0 || err > max_error) continue;
+    if (best < 0 || ms < c[best].ms || (ms == c[best].ms && err < c[best].rel_err)) best = i;
+  }
+  return best;
+}
+
+double sffft_relative_l2(double squared_error, double squared_reference) {
+  if (squared_reference > 0) return std::sqrt(squared_error / squared_reference);
+  return squared_error == 0 ? 0.0 : std::numeric_limits<double>::infinity();
+}
+
+const char* sffft_last_error(void) { return g_last_error; }
+
+const char* sffft_strerror(int code) {
+  switch (code) {
+    case SFFFT_OK: return "success";
+    case SFFFT_EINVAL: return "invalid argument";
+    case SFFFT_ENOPLAN: return "plan not compiled into this library";
+    case SFFFT_EHIP: return "HIP runtime error";
+    case SFFFT_ENOTFOUND: return "not found";
+    default: return "unknown error";
+  }
+}
+
+}  // extern "C"

@@ -1,0 +1,615 @@
+// Fused causal long convolution for AMD Instinct MI355X (gfx950, CDNA4).
+//
+//   y[b,h,n] = sum_{m<=n} u[b,h,m] * k[h,n-m],   n < L
+//
+// computed as a length N = 2L transform, N = R0*R1(*R2), radices 16/32/64,
+// in ONE launch per batch, one workgroup per sequence (NSEQ=1) or per pair of
+// sequences of the same channel packed as the real and imaginary parts of one
+// complex transform (NSEQ=2). Everything between the input load and the output
+// store stays in LDS and VGPRs.
+//
+// Reference behaviour followed (file:line in the reference tree):
+//   plan geometry ............. src/sffft.cu:92-104  (Plan<R0,R1,R2>)
+//   twiddle exponent .......... src/sffft.cu:106-113 (twid<P,J>)
+//   stage schedule ............ src/sffft.cu:273-279 (L0f [L1f] Rf Ri [L1i] L0i)
+//   real-input / real-output .. src/sffft.cu:142-144,164-165,180-181
+//   spectrum fused between the last forward and first inverse stage:
+//                               src/sffft.cu:229-236
+//   fp16 storage, fp32 twiddle/spectrum arithmetic: src/sffft.cu:120-135
+//
+// MI355X design (not a translation of the WMMA code):
+//  * Every stage is a dense complex contraction on v_mfma_f32_16x16x32_f16.
+//    A complex K=16 contraction is one real K=32 contraction: operand slots
+//    0..3 of lane (i, g=lane/16) hold the real parts of complex index 4g..4g+3,
+//    slots 4..7 the imaginary parts, so Dr = [Xr|Xi].[Fr;-Fi] and
+//    Di = [Xr|Xi].[Fi;Fr] are two MFMAs per 16-wide complex K step.
+//  * The MFMA D layout (lane (c,g) holds rows 4g..4g+3 of column c) equals the
+//    A/B operand layout of the next contraction over those rows, so the last
+//    forward stage, the spectrum product and the first inverse stage run in
+//    registers without touching LDS.
+//  * Between stages the LDS layout changes so the next contraction digit is the
+//    fastest one: operand reads and accumulator writes are 8-byte vectors.
+//  * Inverse stages reuse the forward DFT fragments: IDFT(X) = conj(DFT(conj X));
+//    the conjugations are folded into the twiddle and spectrum products.
+//  * Twiddles are computed in registers with v_sin_f32/v_cos_f32 (argument in
+//    revolutions, so e/N is exact) and a 3-step complex recurrence.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace sffft {
+
+typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef float f4 __attribute__((ext_vector_type(4)));
+
+constexpr int LDS_PAD = 4;  // halves appended to each LDS row (keeps 8-byte alignment)
+
+// DFT fragment table (units of h8 = one lane's 8 halves; 64 lanes per fragment).
+//   CF[R][a][b][kind]: complex fragments, lane (r,g), slot v<4:
+//        kind 0: [ cos t | sin t ],  kind 1: [ -sin t | cos t ],
+//        t = 2*pi*((16a+r)*(16b+4g+v) mod R)/R  (F = exp(-i t) is symmetric)
+//   RI[R][nt][kind]: real-input fragments (one sequence), lane (c,g), slot j:
+//        n0 = j<4 ? 4g+j : 16+4g+(j-4),  t = 2*pi*((n0*(16nt+c)) mod R)/R
+//        kind 0: cos t, kind 1: -sin t;  zero for n0 >= R/2 (the zero-padded half)
+__host__ __device__ constexpr int cf_off(int R) { return R == 16 ? 0 : R == 32 ? 256 : 1024; }
+__host__ __device__ constexpr int ri_off(int R) { return R == 16 ? 128 : R == 32 ? 768 : 3072; }
+constexpr int FTAB_H8 = 3584;
+
+__host__ __device__ constexpr int cmax(int a, int b) { return a > b ? a : b; }
+
+template <int R0_, int R1_, int R2_ = 1>
+struct Plan {
+  static constexpr int R0 = R0_, R1 = R1_, R2 = R2_;
+  static constexpr int S = R2_ > 1 ? 3 : 2;
+  static constexpr int N = R0 * R1 * R2, L = N / 2;
+  static constexpr int M = N / R0;           // positions per first-digit row
+  static constexpr int PA = R1 + LDS_PAD;    // pitch: rows whose fastest digit is n1/k1
+  static constexpr int PB = R0 + LDS_PAD;    // pitch: [m][k0], input of the last inverse stage
+  static constexpr int PC = R2 + LDS_PAD;    // pitch: [k1][n2] (three-stage only)
+  static constexpr int ROW = S == 3 ? cmax(R2 * PA, R1 * PC) : 0;
+  static constexpr int PLANE0 = S == 3 ? cmax(R0 * ROW, M * PB) : cmax(R0 * PA, R1 * PB);
+  static constexpr int PLANE = (PLANE0 + 63) & ~63;
+  static constexpr int LDS_BYTES = 2 * PLANE * 2;
+  static_assert(R0 >= 16 && R1 >= 16 && (S == 2 || R2 >= 16), "radices are 16, 32 or 64");
+  static_assert(R0 <= 64 && R1 <= 64 && R2 <= 64, "radices are 16, 32 or 64");
+};
+
+__device__ __forceinline__ f4 mfma(h8 a, h8 b, f4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ float sin_rev(float x) { return __builtin_amdgcn_sinf(x); }  // sin(2*pi*x)
+__device__ __forceinline__ float cos_rev(float x) { return __builtin_amdgcn_cosf(x); }  // cos(2*pi*x)
+
+// ---- I/O element conversions -------------------------------------------------
+__device__ __forceinline__ float io_to_f32(float x) { return x; }
+__device__ __forceinline__ float io_to_f32(uint16_t b) { return __uint_as_float((uint32_t)b << 16); }
+// fp32 -> bf16, IEEE round-to-nearest-even; NaN stays a quiet NaN.
+__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
+  uint32_t x = __float_as_uint(f);
+  if ((x & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((x >> 16) | 0x40u);
+  x += 0x7fffu + ((x >> 16) & 1u);
+  return (uint16_t)(x >> 16);
+}
+// fp16-accumulation mode: the raw tile accumulator is rounded to fp16 (range and
+// rounding of an fp16 accumulator; +-inf beyond 65504).
+__device__ __forceinline__ f4 round_acc(f4 v, int acc16) {
+  if (acc16) {
+#pragma unroll
+    for (int i = 0; i < 4; i++) v[i] = (float)(_Float16)v[i];
+  }
+  return v;
+}
+
+// ---- DFT fragments ------------------------------------------------------------
+template <int R, bool CACHED>
+__device__ __forceinline__ h8 cf_frag(const h8* __restrict__ ftab, int a, int b, int kind, int lane) {
+  if constexpr (CACHED) {
+    return ftab[cf_off(R) + ((a * (R / 16) + b) * 2 + kind) * 64 + lane];
+  } else {
+    const int r = lane & 15, g = lane >> 4;
+    h8 f;
+#pragma unroll
+    for (int v = 0; v < 4; v++) {
+      const int e = ((16 * a + r) * (16 * b + 4 * g + v)) & (R - 1);
+      const float x = (float)e * (1.0f / R);
+      const _Float16 s = (_Float16)sin_rev(x), c = (_Float16)cos_rev(x);
+      f[v] = kind == 0 ? c : -s;
+      f[4 + v] = kind == 0 ? s : c;
+    }
+    return f;
+  }
+}
+template <int R, bool CACHED>
+__device__ __forceinline__ h8 ri_frag(const h8* __restrict__ ftab, int nt, int kind, int lane) {
+  if constexpr (CACHED) {
+    return ftab[ri_off(R) + (nt * 2 + kind) * 64 + lane];
+  } else {
+    const int c = lane & 15, g = lane >> 4;
+    h8 f;
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+      const int n0 = j < 4 ? 4 * g + j : 16 + 4 * g + (j - 4);
+      const int e = (n0 * (16 * nt + c)) & (R - 1);
+      const float x = (float)e * (1.0f / R);
+      f[j] = n0 >= R / 2 ? (_Float16)0.f : kind == 0 ? (_Float16)cos_rev(x) : -(_Float16)sin_rev(x);
+    }
+    return f;
+  }
+}
+
+// w[v] = sc * exp(-2*pi*i * a*(b0+v) / N), v = 0..3 (src/sffft.cu:106-113 for the
+// exponent; the angle is reduced to (-1/2, 1/2] revolutions before v_sin/v_cos).
+template <int N>
+__device__ __forceinline__ void twiddle4(int a, int b0, float sc, float* wr, float* wi) {
+  const int e0 = (a * b0) & (N - 1), e1 = a & (N - 1);
+  const float x0 = (float)(e0 > N / 2 ? e0 - N : e0) * (1.0f / N);
+  const float x1 = (float)(e1 > N / 2 ? e1 - N : e1) * (1.0f / N);
+  float r = sc * cos_rev(x0), i = -sc * sin_rev(x0);
+  const float sr = cos_rev(x1), si = -sin_rev(x1);
+  wr[0] = r;
+  wi[0] = i;
+#pragma unroll
+  for (int v = 1; v < 4; v++) {
+    const float nr = r * sr - i * si, ni = r * si + i * sr;
+    r = nr;
+    i = ni;
+    wr[v] = r;
+    wi[v] = i;
+  }
+}
+
+// 8-half operand: slots 0..3 from the real plane, 4..7 from the imaginary plane.
+__device__ __forceinline__ h8 lds_frag(const _Float16* re, const _Float16* im, int pos) {
+  const h4 a = *reinterpret_cast<const h4*>(re + pos);
+  const h4 b = *reinterpret_cast<const h4*>(im + pos);
+  return (h8){a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
+}
+__device__ __forceinline__ h4 to_h4(const float* x) {
+  return (h4){(_Float16)x[0], (_Float16)x[1], (_Float16)x[2], (_Float16)x[3]};
+}
+
+__device__ __forceinline__ void wave_sync() {
+  // LDS operations of one wavefront execute in order; this keeps the compiler
+  // from moving LDS accesses across the point where lanes exchange data.
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// ---- Phase 1: first forward stage over n0 (src/sffft.cu:266-274) ---------------
+// Input rows are natural order, n = n0*M + m. Data is the A operand (M = 16
+// consecutive m, K = n0); only n0 < R0/2 is loaded (the zero-padded half is
+// skipped). Output D[m][k0] is twiddled by w^(k0*m) and written with m fastest.
+template <class P, int NSEQ, class TIO>
+__device__ __forceinline__ void p1_load(const TIO* __restrict__ xa, const TIO* __restrict__ xb, int mt,
+                                        h8* a, int r, int g) {
+  constexpr int R0 = P::R0, M = P::M;
+  constexpr int KS = NSEQ == 2 ? (R0 / 2 + 15) / 16 : 1;
+  const int m = 16 * mt + r;
+#pragma unroll
+  for (int ks = 0; ks < KS; ks++) {
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+      int n0;
+      const TIO* src;
+      if constexpr (NSEQ == 2) {
+        n0 = 16 * ks + 4 * g + (j & 3);
+        src = j < 4 ? xa : xb;
+      } else {
+        n0 = j < 4 ? 4 * g + j : 16 + 4 * g + (j - 4);
+        src = xa;
+      }
+      float v = 0.f;
+      if (n0 < R0 / 2) v = io_to_f32(src[n0 * M + m]);
+      a[ks][j] = (_Float16)v;
+    }
+  }
+}
+
+template <class P, int NW, int NSEQ, class TIO, bool CACHED>
+__device__ __forceinline__ void phase1(const TIO* __restrict__ xa, const TIO* __restrict__ xb, _Float16* re,
+                                       _Float16* im, const h8* __restrict__ ftab, int acc16, int lane, int wave) {
+  constexpr int R0 = P::R0, N = P::N, MT = P::M / 16, NT = R0 / 16;
+  constexpr int KS = NSEQ == 2 ? (R0 / 2 + 15) / 16 : 1;
+  constexpr float sc0 = R0 == 16 ? 0.25f : R0 == 32 ? 0.17677669529663687f : 0.125f;
+  const int r = lane & 15, g = lane >> 4;
+  auto tile = [&](const h8* a, int mt, int nt) {
+    f4 dr = {0.f, 0.f, 0.f, 0.f}, di = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int ks = 0; ks < KS; ks++) {
+      if constexpr (NSEQ == 2) {
+        dr = mfma(a[ks], cf_frag<R0, CACHED>(ftab, nt, ks, 0, lane), dr);
+        di = mfma(a[ks], cf_frag<R0, CACHED>(ftab, nt, ks, 1, lane), di);
+      } else {
+        dr = mfma(a[ks], ri_frag<R0, CACHED>(ftab, nt, 0, lane), dr);
+        di = mfma(a[ks], ri_frag<R0, CACHED>(ftab, nt, 1, lane), di);
+      }
+    }
+    dr = round_acc(dr, acc16);
+    di = round_acc(di, acc16);
+    const int k0 = 16 * nt + r;
+    float wr[4], wi[4], xr[4], xi[4];
+    twiddle4<N>(k0, 16 * mt + 4 * g, sc0, wr, wi);
+#pragma unroll
+    for (int v = 0; v < 4; v++) {
+      xr[v] = dr[v] * wr[v] - di[v] * wi[v];
+      xi[v] = dr[v] * wi[v] + di[v] * wr[v];
+    }
+    if constexpr (P::S == 2) {
+      const int pos = k0 * P::PA + 16 * mt + 4 * g;  // [k0][n1]
+      *reinterpret_cast<h4*>(re + pos) = to_h4(xr);
+      *reinterpret_cast<h4*>(im + pos) = to_h4(xi);
+    } else {
+#pragma unroll
+      for (int v = 0; v < 4; v++) {  // [k0][n2][n1]
+        const int m = 16 * mt + 4 * g + v, n1 = m / P::R2, n2 = m % P::R2;
+        const int pos = k0 * P::ROW + n2 * P::PA + n1;
+        re[pos] = (_Float16)xr[v];
+        im[pos] = (_Float16)xi[v];
+      }
+    }
+  };
+  if constexpr (MT >= NW) {
+    for (int mt = wave; mt < MT; mt += NW) {
+      h8 a[KS];
+      p1_load<P, NSEQ, TIO>(xa, xb, mt, a, r, g);
+#pragma unroll
+      for (int nt = 0; nt < NT; nt++) tile(a, mt, nt);
+    }
+  } else {
+    for (int u = wave; u < MT * NT; u += NW) {
+      const int mt = u / NT, nt = u % NT;
+      h8 a[KS];
+      p1_load<P, NSEQ, TIO>(xa, xb, mt, a, r, g);
+      tile(a, mt, nt);
+    }
+  }
+}
+
+// ---- Spectrum product + first inverse stage (src/sffft.cu:229-236, 276-277) -----
+// d = forward result tiles D[kk][c] (lane column c, rows 16*mt+4g+v), K = kernel
+// order spectrum for this unit. Returns A operands conj(D*K)^T for the inverse.
+template <int T>
+__device__ __forceinline__ void spectrum_product(const f4* dr, const f4* di, const float2* __restrict__ kp,
+                                                 int lane, h8* a2) {
+#pragma unroll
+  for (int mt = 0; mt < T; mt++) {
+    const float4* q = reinterpret_cast<const float4*>(kp + (mt * 64 + lane) * 4);
+    const float4 k01 = q[0], k23 = q[1];
+    const float kr[4] = {k01.x, k01.z, k23.x, k23.z};
+    const float ki[4] = {k01.y, k01.w, k23.y, k23.w};
+#pragma unroll
+    for (int v = 0; v < 4; v++) {
+      const float xr = dr[mt][v] * kr[v] - di[mt][v] * ki[v];
+      const float xi = dr[mt][v] * ki[v] + di[mt][v] * kr[v];
+      a2[mt][v] = (_Float16)xr;
+      a2[mt][4 + v] = (_Float16)(-xi);
+    }
+  }
+}
+
+// ---- Phase 2, two-stage plans: over n1, spectrum, inverse over k1 ----------------
+template <class P, int NW, bool CACHED>
+__device__ __forceinline__ void phase2_s2(_Float16* re, _Float16* im, const float2* __restrict__ K,
+                                          const h8* __restrict__ ftab, int acc16, int lane, int wave) {
+  constexpr int R0 = P::R0, R1 = P::R1, N = P::N, ST = R0 / 16, T1 = R1 / 16;
+  constexpr int UPW = (ST + NW - 1) / NW;
+  constexpr float sc1 = R1 == 16 ? 0.25f : R1 == 32 ? 0.17677669529663687f : 0.125f;
+  const int c = lane & 15, g = lane >> 4;
+  h4 outr[UPW][T1], outi[UPW][T1];
+#pragma unroll
+  for (int i = 0; i < UPW; i++) {
+    const int s = wave + i * NW;
+    if (s < ST) {
+      h8 b[T1];
+#pragma unroll
+      for (int ks = 0; ks < T1; ks++) b[ks] = lds_frag(re, im, (16 * s + c) * P::PA + 16 * ks + 4 * g);
+      f4 dr[T1], di[T1];
+#pragma unroll
+      for (int mt = 0; mt < T1; mt++) {
+        dr[mt] = (f4){0.f, 0.f, 0.f, 0.f};
+        di[mt] = (f4){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int ks = 0; ks < T1; ks++) {
+          dr[mt] = mfma(cf_frag<R1, CACHED>(ftab, mt, ks, 0, lane), b[ks], dr[mt]);
+          di[mt] = mfma(cf_frag<R1, CACHED>(ftab, mt, ks, 1, lane), b[ks], di[mt]);
+        }
+        dr[mt] = round_acc(dr[mt], acc16);
+        di[mt] = round_acc(di[mt], acc16);
+      }
+      h8 a2[T1];
+      spectrum_product<T1>(dr, di, K + (size_t)s * T1 * 256, lane, a2);
+#pragma unroll
+      for (int nt = 0; nt < T1; nt++) {
+        f4 er = {0.f, 0.f, 0.f, 0.f}, ei = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int mt = 0; mt < T1; mt++) {
+          er = mfma(a2[mt], cf_frag<R1, CACHED>(ftab, nt, mt, 0, lane), er);
+          ei = mfma(a2[mt], cf_frag<R1, CACHED>(ftab, nt, mt, 1, lane), ei);
+        }
+        er = round_acc(er, acc16);
+        ei = round_acc(ei, acc16);
+        float wr[4], wi[4], xr[4], xi[4];
+        twiddle4<N>(16 * nt + c, 16 * s + 4 * g, sc1, wr, wi);
+#pragma unroll
+        for (int v = 0; v < 4; v++) {
+          xr[v] = er[v] * wr[v] - ei[v] * wi[v];
+          xi[v] = er[v] * wi[v] + ei[v] * wr[v];
+        }
+        outr[i][nt] = to_h4(xr);
+        outi[i][nt] = to_h4(xi);
+      }
+    }
+  }
+  __syncthreads();  // every strip has been read before the [n1][k0] layout is written
+#pragma unroll
+  for (int i = 0; i < UPW; i++) {
+    const int s = wave + i * NW;
+    if (s < ST) {
+#pragma unroll
+      for (int nt = 0; nt < T1; nt++) {
+        const int pos = (16 * nt + c) * P::PB + 16 * s + 4 * g;
+        *reinterpret_cast<h4*>(re + pos) = outr[i][nt];
+        *reinterpret_cast<h4*>(im + pos) = outi[i][nt];
+      }
+    }
+  }
+}
+
+// ---- Phase 2, three-stage plans: per k0 row, stages over n1 and n2, spectrum,
+// inverse over k2 and k1. A row is owned by one wave; only wave-level ordering
+// is needed until the final [m][k0] write.
+template <class P, int NW, bool CACHED>
+__device__ __forceinline__ void phase2_s3(_Float16* re, _Float16* im, const float2* __restrict__ K,
+                                          const h8* __restrict__ ftab, int acc16, int lane, int wave) {
+  constexpr int R0 = P::R0, R1 = P::R1, R2 = P::R2, N = P::N, T1 = R1 / 16, T2 = R2 / 16;
+  constexpr int ROWS = R0 / NW;
+  static_assert(R0 % NW == 0, "three-stage plans need R0 divisible by the wave count");
+  constexpr float sc1 = R1 == 16 ? 0.25f : R1 == 32 ? 0.17677669529663687f : 0.125f;
+  constexpr float sc2 = R2 == 16 ? 0.25f : R2 == 32 ? 0.17677669529663687f : 0.125f;
+  const int c = lane & 15, g = lane >> 4;
+  h4 outr[ROWS][T2][T1], outi[ROWS][T2][T1];
+#pragma unroll
+  for (int i = 0; i < ROWS; i++) {
+    const int k0 = wave + i * NW;
+    const int rb = k0 * P::ROW;
+    {  // stage over n1: [n2][n1] -> [k1][n2]
+      h8 a[T2][T1];
+#pragma unroll
+      for (int t2 = 0; t2 < T2; t2++)
+#pragma unroll
+        for (int ks = 0; ks < T1; ks++) a[t2][ks] = lds_frag(re, im, rb + (16 * t2 + c) * P::PA + 16 * ks + 4 * g);
+#pragma unroll
+      for (int t2 = 0; t2 < T2; t2++) {
+#pragma unroll
+        for (int nt = 0; nt < T1; nt++) {
+          f4 dr = {0.f, 0.f, 0.f, 0.f}, di = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int ks = 0; ks < T1; ks++) {
+            dr = mfma(a[t2][ks], cf_frag<R1, CACHED>(ftab, nt, ks, 0, lane), dr);
+            di = mfma(a[t2][ks], cf_frag<R1, CACHED>(ftab, nt, ks, 1, lane), di);
+          }
+          dr = round_acc(dr, acc16);
+          di = round_acc(di, acc16);
+          float wr[4], wi[4], xr[4], xi[4];
+          twiddle4<N>(R0 * (16 * nt + c), 16 * t2 + 4 * g, sc1, wr, wi);
+#pragma unroll
+          for (int v = 0; v < 4; v++) {
+            xr[v] = dr[v] * wr[v] - di[v] * wi[v];
+            xi[v] = dr[v] * wi[v] + di[v] * wr[v];
+          }
+          const int pos = rb + (16 * nt + c) * P::PC + 16 * t2 + 4 * g;
+          *reinterpret_cast<h4*>(re + pos) = to_h4(xr);
+          *reinterpret_cast<h4*>(im + pos) = to_h4(xi);
+        }
+      }
+    }
+    wave_sync();
+    {  // stage over n2, spectrum, inverse over k2: [k1][n2] -> conj, [n2][k1]
+      h8 b[T1][T2];
+#pragma unroll
+      for (int t1 = 0; t1 < T1; t1++)
+#pragma unroll
+        for (int ks = 0; ks < T2; ks++) b[t1][ks] = lds_frag(re, im, rb + (16 * t1 + c) * P::PC + 16 * ks + 4 * g);
+#pragma unroll
+      for (int t1 = 0; t1 < T1; t1++) {
+        f4 dr[T2], di[T2];
+#pragma unroll
+        for (int mt = 0; mt < T2; mt++) {
+          dr[mt] = (f4){0.f, 0.f, 0.f, 0.f};
+          di[mt] = (f4){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int ks = 0; ks < T2; ks++) {
+            dr[mt] = mfma(cf_frag<R2, CACHED>(ftab, mt, ks, 0, lane), b[t1][ks], dr[mt]);
+            di[mt] = mfma(cf_frag<R2, CACHED>(ftab, mt, ks, 1, lane), b[t1][ks], di[mt]);
+          }
+          dr[mt] = round_acc(dr[mt], acc16);
+          di[mt] = round_acc(di[mt], acc16);
+        }
+        h8 a2[T2];
+        spectrum_product<T2>(dr, di, K + (size_t)(k0 * T1 + t1) * T2 * 256, lane, a2);
+#pragma unroll
+        for (int nt = 0; nt < T2; nt++) {
+          f4 er = {0.f, 0.f, 0.f, 0.f}, ei = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int mt = 0; mt < T2; mt++) {
+            er = mfma(a2[mt], cf_frag<R2, CACHED>(ftab, nt, mt, 0, lane), er);
+            ei = mfma(a2[mt], cf_frag<R2, CACHED>(ftab, nt, mt, 1, lane), ei);
+          }
+          er = round_acc(er, acc16);
+          ei = round_acc(ei, acc16);
+          float wr[4], wi[4], xr[4], xi[4];
+          twiddle4<N>(R0 * (16 * nt + c), 16 * t1 + 4 * g, sc2, wr, wi);
+#pragma unroll
+          for (int v = 0; v < 4; v++) {
+            xr[v] = er[v] * wr[v] - ei[v] * wi[v];
+            xi[v] = er[v] * wi[v] + ei[v] * wr[v];
+          }
+          const int pos = rb + (16 * nt + c) * P::PA + 16 * t1 + 4 * g;
+          *reinterpret_cast<h4*>(re + pos) = to_h4(xr);
+          *reinterpret_cast<h4*>(im + pos) = to_h4(xi);
+        }
+      }
+    }
+    wave_sync();
+    {  // inverse over k1: [n2][k1] -> staged, written as [m][k0]
+      h8 a[T2][T1];
+#pragma unroll
+      for (int t2 = 0; t2 < T2; t2++)
+#pragma unroll
+        for (int ks = 0; ks < T1; ks++) a[t2][ks] = lds_frag(re, im, rb + (16 * t2 + c) * P::PA + 16 * ks + 4 * g);
+#pragma unroll
+      for (int t2 = 0; t2 < T2; t2++) {
+#pragma unroll
+        for (int nt = 0; nt < T1; nt++) {
+          f4 er = {0.f, 0.f, 0.f, 0.f}, ei = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int ks = 0; ks < T1; ks++) {
+            er = mfma(a[t2][ks], cf_frag<R1, CACHED>(ftab, nt, ks, 0, lane), er);
+            ei = mfma(a[t2][ks], cf_frag<R1, CACHED>(ftab, nt, ks, 1, lane), ei);
+          }
+          er = round_acc(er, acc16);
+          ei = round_acc(ei, acc16);
+          float wr[4], wi[4], xr[4], xi[4];
+          twiddle4<N>(k0, (16 * nt + c) * R2 + 16 * t2 + 4 * g, sc1, wr, wi);
+#pragma unroll
+          for (int v = 0; v < 4; v++) {
+            xr[v] = er[v] * wr[v] - ei[v] * wi[v];
+            xi[v] = er[v] * wi[v] + ei[v] * wr[v];
+          }
+          outr[i][t2][nt] = to_h4(xr);
+          outi[i][t2][nt] = to_h4(xi);
+        }
+      }
+    }
+    wave_sync();
+  }
+  __syncthreads();  // every row has been read before the [m][k0] layout is written
+#pragma unroll
+  for (int i = 0; i < ROWS; i++) {
+    const int k0 = wave + i * NW;
+#pragma unroll
+    for (int t2 = 0; t2 < T2; t2++)
+#pragma unroll
+      for (int nt = 0; nt < T1; nt++) {
+        const int m0 = (16 * nt + c) * R2 + 16 * t2 + 4 * g;
+#pragma unroll
+        for (int v = 0; v < 4; v++) {
+          re[(m0 + v) * P::PB + k0] = outr[i][t2][nt][v];
+          im[(m0 + v) * P::PB + k0] = outi[i][t2][nt][v];
+        }
+      }
+  }
+}
+
+// ---- Phase 3: last inverse stage over k0, first L outputs only -----------------
+// (src/sffft.cu:144,165,180-181,279). Reads conj(W)[m][k0]; y = Re of the inverse
+// (the second sequence of a pair is the imaginary part).
+template <class P, int NW, int NSEQ, class TIO, bool CACHED>
+__device__ __forceinline__ void phase3(TIO* __restrict__ ya, TIO* __restrict__ yb, const _Float16* re,
+                                       const _Float16* im, const h8* __restrict__ ftab, int acc16, int lane,
+                                       int wave) {
+  constexpr int R0 = P::R0, M = P::M, MT = M / 16, NT = R0 >= 32 ? R0 / 32 : 1, KS = R0 / 16;
+  constexpr float sc0 = R0 == 16 ? 0.25f : R0 == 32 ? 0.17677669529663687f : 0.125f;
+  const int r = lane & 15, g = lane >> 4;
+  auto tile = [&](const h8* a, int mt, int nt) {
+    f4 zr = {0.f, 0.f, 0.f, 0.f}, zi = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int ks = 0; ks < KS; ks++) {
+      zr = mfma(a[ks], cf_frag<R0, CACHED>(ftab, nt, ks, 0, lane), zr);
+      if constexpr (NSEQ == 2) zi = mfma(a[ks], cf_frag<R0, CACHED>(ftab, nt, ks, 1, lane), zi);
+    }
+    zr = round_acc(zr, acc16);
+    if constexpr (NSEQ == 2) zi = round_acc(zi, acc16);
+    const int n0 = 16 * nt + r;
+    if (n0 < R0 / 2) {
+      const int o = n0 * M + 16 * mt + 4 * g;
+      if constexpr (sizeof(TIO) == 4) {
+        *reinterpret_cast<float4*>(ya + o) = make_float4(zr[0] * sc0, zr[1] * sc0, zr[2] * sc0, zr[3] * sc0);
+        if constexpr (NSEQ == 2)
+          *reinterpret_cast<float4*>(yb + o) =
+              make_float4(-zi[0] * sc0, -zi[1] * sc0, -zi[2] * sc0, -zi[3] * sc0);
+      } else {
+        uint2 q;
+        q.x = (uint32_t)f32_to_bf16(zr[0] * sc0) | ((uint32_t)f32_to_bf16(zr[1] * sc0) << 16);
+        q.y = (uint32_t)f32_to_bf16(zr[2] * sc0) | ((uint32_t)f32_to_bf16(zr[3] * sc0) << 16);
+        *reinterpret_cast<uint2*>(ya + o) = q;
+        if constexpr (NSEQ == 2) {
+          q.x = (uint32_t)f32_to_bf16(-zi[0] * sc0) | ((uint32_t)f32_to_bf16(-zi[1] * sc0) << 16);
+          q.y = (uint32_t)f32_to_bf16(-zi[2] * sc0) | ((uint32_t)f32_to_bf16(-zi[3] * sc0) << 16);
+          *reinterpret_cast<uint2*>(yb + o) = q;
+        }
+      }
+    }
+  };
+  auto load = [&](int mt, h8* a) {
+#pragma unroll
+    for (int ks = 0; ks < KS; ks++) a[ks] = lds_frag(re, im, (16 * mt + r) * P::PB + 16 * ks + 4 * g);
+  };
+  if constexpr (MT >= NW) {
+    for (int mt = wave; mt < MT; mt += NW) {
+      h8 a[KS];
+      load(mt, a);
+#pragma unroll
+      for (int nt = 0; nt < NT; nt++) tile(a, mt, nt);
+    }
+  } else {
+    for (int u = wave; u < MT * NT; u += NW) {
+      const int mt = u / NT, nt = u % NT;
+      h8 a[KS];
+      load(mt, a);
+      tile(a, mt, nt);
+    }
+  }
+}
+
+// ---- The fused kernel (src/sffft.cu:243-280) ------------------------------------
+// grid = H * (B / NSEQ) workgroups, batch index fastest (block -> (h, b) as in
+// src/sffft.cu:249) so the B/NSEQ workgroups of one channel run back to back and
+// share that channel's spectrum in cache.
+template <class P, int NW, int NSEQ, class TIO, bool CACHED>
+__global__ void __launch_bounds__(64 * NW)
+    fftconv_kernel(const TIO* __restrict__ u, const float2* __restrict__ kf, TIO* __restrict__ y, int B, int H,
+                   const h8* __restrict__ ftab, int acc16) {
+  __shared__ __attribute__((aligned(16))) _Float16 lds[2 * P::PLANE];
+  _Float16* re = lds;
+  _Float16* im = lds + P::PLANE;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int BP = B / NSEQ;
+  const int h = blockIdx.x / BP, bp = blockIdx.x - h * BP;
+  const size_t row_a = ((size_t)(bp * NSEQ) * H + h) * P::L;
+  const size_t row_b = NSEQ == 2 ? row_a + (size_t)H * P::L : row_a;
+  const float2* K = kf + (size_t)h * P::N;
+  phase1<P, NW, NSEQ, TIO, CACHED>(u + row_a, u + row_b, re, im, ftab, acc16, lane, wave);
+  __syncthreads();
+  if constexpr (P::S == 2)
+    phase2_s2<P, NW, CACHED>(re, im, K, ftab, acc16, lane, wave);
+  else
+    phase2_s3<P, NW, CACHED>(re, im, K, ftab, acc16, lane, wave);
+  __syncthreads();
+  phase3<P, NW, NSEQ, TIO, CACHED>(y + row_a, y + row_b, re, im, ftab, acc16, lane, wave);
+}
+
+// Kernel-order spectrum index -> digits (k0, k1, k2) of the frequency
+// k = k0 + R0*k1 + R0*R1*k2 (the digit order of src/sffft.cu:283-288, laid out
+// in the register order in which the fused kernel consumes it).
+template <class P>
+__host__ __device__ inline void kernel_order_digits(int idx, int& k0, int& k1, int& k2) {
+  const int v = idx & 3, lane = (idx >> 2) & 63, rest = idx >> 8;
+  const int c = lane & 15, g = lane >> 4;
+  if constexpr (P::S == 2) {
+    const int T1 = P::R1 / 16, mt = rest % T1, s = rest / T1;
+    k0 = 16 * s + c;
+    k1 = 16 * mt + 4 * g + v;
+    k2 = 0;
+  } else {
+    const int T1 = P::R1 / 16, T2 = P::R2 / 16;
+    const int mt = rest % T2, t1 = (rest / T2) % T1;
+    k0 = rest / (T2 * T1);
+    k1 = 16 * t1 + c;
+    k2 = 16 * mt + 4 * g + v;
+  }
+}
+
+}  // namespace sffft

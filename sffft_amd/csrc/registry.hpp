@@ -1,0 +1,28 @@
+// Compiled-plan registry shared by the per-length instantiation units and the C ABI.
+#pragma once
+#include <hip/hip_runtime.h>
+
+namespace sffft {
+
+typedef hipError_t (*launch_fn)(const void* u, const void* kf, void* y, int B, int H, const void* ftab, int acc16,
+                                hipStream_t stream);
+
+// One (plan, waves, sequences-per-workgroup) instantiation: launchers and kernel
+// symbols for [io: 0 = fp32, 1 = bf16][cached: 0 = in-kernel DFT matrices, 1 = table].
+struct Entry {
+  int L, r0, r1, r2, waves, seqs, lds_bytes;
+  launch_fn launch[2][2];
+  const void* func[2][2];
+};
+
+// Defined by conv_inst.hip compiled once per length.
+const Entry* entries_L128(int* n);
+const Entry* entries_L256(int* n);
+const Entry* entries_L512(int* n);
+const Entry* entries_L1024(int* n);
+const Entry* entries_L2048(int* n);
+const Entry* entries_L4096(int* n);
+const Entry* entries_L8192(int* n);
+const Entry* entries_L16384(int* n);
+
+}  // namespace sffft
