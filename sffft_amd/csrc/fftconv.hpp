@@ -181,6 +181,26 @@ __device__ __forceinline__ void wave_sync() {
 // Input rows are natural order, n = n0*M + m. Data is the A operand (M = 16
 // consecutive m, K = n0); only n0 < R0/2 is loaded (the zero-padded half is
 // skipped). Output D[m][k0] is twiddled by w^(k0*m) and written with m fastest.
+// Work split: the A tiles (16 consecutive m) are spread over the waves; when there
+// are fewer A tiles than waves, the waves sharing a tile split its k0 tiles, so
+// every input element is loaded by exactly one wave.
+template <class P, int NW, int NSEQ>
+struct P1Split {
+  static constexpr int MT = P::M / 16, NT = P::R0 / 16;
+  static constexpr bool BY_MT = MT >= NW;
+  static constexpr int TPW = BY_MT ? MT / NW : 1;                // A tiles per wave
+  static constexpr int WPM = BY_MT ? 1 : NW / MT;                // waves sharing one A tile
+  static constexpr int NTW = BY_MT ? NT : (NT + WPM - 1) / WPM;  // k0 tiles per A tile and wave
+  static constexpr int KS = NSEQ == 2 ? (P::R0 / 2 + 15) / 16 : 1;  // K steps
+  __device__ static int mt(int wave, int i) { return BY_MT ? wave + i * NW : wave % MT; }
+  __device__ static int nt(int wave, int j) { return BY_MT ? j : wave / MT + j * WPM; }
+};
+
+template <class P, int NW, int NSEQ>
+struct P1Data {
+  h8 a[P1Split<P, NW, NSEQ>::TPW][P1Split<P, NW, NSEQ>::KS];
+};
+
 template <class P, int NSEQ, class TIO>
 __device__ __forceinline__ void p1_load(const TIO* __restrict__ xa, const TIO* __restrict__ xb, int mt,
                                         h8* a, int r, int g) {
@@ -207,76 +227,83 @@ __device__ __forceinline__ void p1_load(const TIO* __restrict__ xa, const TIO* _
   }
 }
 
-template <class P, int NW, int NSEQ, class TIO, bool CACHED>
-__device__ __forceinline__ void phase1(const TIO* __restrict__ xa, const TIO* __restrict__ xb, _Float16* re,
-                                       _Float16* im, const h8* __restrict__ ftab, int acc16, int lane, int wave) {
-  constexpr int R0 = P::R0, N = P::N, MT = P::M / 16, NT = R0 / 16;
-  constexpr int KS = NSEQ == 2 ? (R0 / 2 + 15) / 16 : 1;
+// Issues every input load of this wave's phase-1 tiles (one HBM round trip).
+template <class P, int NW, int NSEQ, class TIO>
+__device__ __forceinline__ void p1_prefetch(const TIO* __restrict__ xa, const TIO* __restrict__ xb,
+                                            P1Data<P, NW, NSEQ>& d, int lane, int wave) {
+  using SP = P1Split<P, NW, NSEQ>;
+#pragma unroll
+  for (int i = 0; i < SP::TPW; i++) p1_load<P, NSEQ, TIO>(xa, xb, SP::mt(wave, i), d.a[i], lane & 15, lane >> 4);
+}
+
+template <class P, int NW, int NSEQ, bool CACHED>
+__device__ __forceinline__ void phase1(const P1Data<P, NW, NSEQ>& d, _Float16* re, _Float16* im,
+                                       const h8* __restrict__ ftab, int acc16, int lane, int wave) {
+  using SP = P1Split<P, NW, NSEQ>;
+  constexpr int R0 = P::R0, N = P::N, KS = SP::KS;
   constexpr float sc0 = R0 == 16 ? 0.25f : R0 == 32 ? 0.17677669529663687f : 0.125f;
   const int r = lane & 15, g = lane >> 4;
-  auto tile = [&](const h8* a, int mt, int nt) {
-    f4 dr = {0.f, 0.f, 0.f, 0.f}, di = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int ks = 0; ks < KS; ks++) {
-      if constexpr (NSEQ == 2) {
-        dr = mfma(a[ks], cf_frag<R0, CACHED>(ftab, nt, ks, 0, lane), dr);
-        di = mfma(a[ks], cf_frag<R0, CACHED>(ftab, nt, ks, 1, lane), di);
-      } else {
-        dr = mfma(a[ks], ri_frag<R0, CACHED>(ftab, nt, 0, lane), dr);
-        di = mfma(a[ks], ri_frag<R0, CACHED>(ftab, nt, 1, lane), di);
+  for (int i = 0; i < SP::TPW; i++) {
+    const int mt = SP::mt(wave, i);
+#pragma unroll
+    for (int j = 0; j < SP::NTW; j++) {
+      const int nt = SP::nt(wave, j);
+      if (nt < SP::NT) {
+        f4 dr = {0.f, 0.f, 0.f, 0.f}, di = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int ks = 0; ks < KS; ks++) {
+          if constexpr (NSEQ == 2) {
+            dr = mfma(d.a[i][ks], cf_frag<R0, CACHED>(ftab, nt, ks, 0, lane), dr);
+            di = mfma(d.a[i][ks], cf_frag<R0, CACHED>(ftab, nt, ks, 1, lane), di);
+          } else {
+            dr = mfma(d.a[i][ks], ri_frag<R0, CACHED>(ftab, nt, 0, lane), dr);
+            di = mfma(d.a[i][ks], ri_frag<R0, CACHED>(ftab, nt, 1, lane), di);
+          }
+        }
+        dr = round_acc(dr, acc16);
+        di = round_acc(di, acc16);
+        const int k0 = 16 * nt + r;
+        float wr[4], wi[4], xr[4], xi[4];
+        twiddle4<N>(k0, 16 * mt + 4 * g, sc0, wr, wi);
+#pragma unroll
+        for (int v = 0; v < 4; v++) {
+          xr[v] = dr[v] * wr[v] - di[v] * wi[v];
+          xi[v] = dr[v] * wi[v] + di[v] * wr[v];
+        }
+        if constexpr (P::S == 2) {
+          const int pos = k0 * P::PA + 16 * mt + 4 * g;  // [k0][n1]
+          *reinterpret_cast<h4*>(re + pos) = to_h4(xr);
+          *reinterpret_cast<h4*>(im + pos) = to_h4(xi);
+        } else {
+#pragma unroll
+          for (int v = 0; v < 4; v++) {  // [k0][n2][n1]
+            const int m = 16 * mt + 4 * g + v, n1 = m / P::R2, n2 = m % P::R2;
+            const int pos = k0 * P::ROW + n2 * P::PA + n1;
+            re[pos] = (_Float16)xr[v];
+            im[pos] = (_Float16)xi[v];
+          }
+        }
       }
-    }
-    dr = round_acc(dr, acc16);
-    di = round_acc(di, acc16);
-    const int k0 = 16 * nt + r;
-    float wr[4], wi[4], xr[4], xi[4];
-    twiddle4<N>(k0, 16 * mt + 4 * g, sc0, wr, wi);
-#pragma unroll
-    for (int v = 0; v < 4; v++) {
-      xr[v] = dr[v] * wr[v] - di[v] * wi[v];
-      xi[v] = dr[v] * wi[v] + di[v] * wr[v];
-    }
-    if constexpr (P::S == 2) {
-      const int pos = k0 * P::PA + 16 * mt + 4 * g;  // [k0][n1]
-      *reinterpret_cast<h4*>(re + pos) = to_h4(xr);
-      *reinterpret_cast<h4*>(im + pos) = to_h4(xi);
-    } else {
-#pragma unroll
-      for (int v = 0; v < 4; v++) {  // [k0][n2][n1]
-        const int m = 16 * mt + 4 * g + v, n1 = m / P::R2, n2 = m % P::R2;
-        const int pos = k0 * P::ROW + n2 * P::PA + n1;
-        re[pos] = (_Float16)xr[v];
-        im[pos] = (_Float16)xi[v];
-      }
-    }
-  };
-  if constexpr (MT >= NW) {
-    for (int mt = wave; mt < MT; mt += NW) {
-      h8 a[KS];
-      p1_load<P, NSEQ, TIO>(xa, xb, mt, a, r, g);
-#pragma unroll
-      for (int nt = 0; nt < NT; nt++) tile(a, mt, nt);
-    }
-  } else {
-    for (int u = wave; u < MT * NT; u += NW) {
-      const int mt = u / NT, nt = u % NT;
-      h8 a[KS];
-      p1_load<P, NSEQ, TIO>(xa, xb, mt, a, r, g);
-      tile(a, mt, nt);
     }
   }
 }
 
 // ---- Spectrum product + first inverse stage (src/sffft.cu:229-236, 276-277) -----
-// d = forward result tiles D[kk][c] (lane column c, rows 16*mt+4g+v), K = kernel
-// order spectrum for this unit. Returns A operands conj(D*K)^T for the inverse.
+// The spectrum tile of one lane: 4 complex64 values, rows 4g..4g+3 of column c of
+// a 16x16 tile, stored contiguously in the kernel order (32 bytes per lane).
+__device__ __forceinline__ void load_k4(const float2* __restrict__ kp, int lane, float4* q) {
+  const float4* p = reinterpret_cast<const float4*>(kp + lane * 4);
+  q[0] = p[0];
+  q[1] = p[1];
+}
+// d = forward result tiles D[kk][c] (lane column c, rows 16*mt+4g+v), q = spectrum
+// tiles. Returns A operands conj(D*K)^T for the inverse.
 template <int T>
-__device__ __forceinline__ void spectrum_product(const f4* dr, const f4* di, const float2* __restrict__ kp,
-                                                 int lane, h8* a2) {
+__device__ __forceinline__ void spectrum_product(const f4* dr, const f4* di, const float4 (*q)[2], h8* a2) {
 #pragma unroll
   for (int mt = 0; mt < T; mt++) {
-    const float4* q = reinterpret_cast<const float4*>(kp + (mt * 64 + lane) * 4);
-    const float4 k01 = q[0], k23 = q[1];
+    const float4 k01 = q[mt][0], k23 = q[mt][1];
     const float kr[4] = {k01.x, k01.z, k23.x, k23.z};
     const float ki[4] = {k01.y, k01.w, k23.y, k23.w};
 #pragma unroll
@@ -290,8 +317,28 @@ __device__ __forceinline__ void spectrum_product(const f4* dr, const f4* di, con
 }
 
 // ---- Phase 2, two-stage plans: over n1, spectrum, inverse over k1 ----------------
+template <class P, int NW>
+struct KData2 {
+  static constexpr int ST = P::R0 / 16, T1 = P::R1 / 16, UPW = (ST + NW - 1) / NW;
+  float4 q[UPW][T1][2];
+};
+
+// Issues the spectrum loads of this wave's strips (kernel order, 1 KB per wave and tile).
+template <class P, int NW>
+__device__ __forceinline__ void k_prefetch_s2(const float2* __restrict__ K, KData2<P, NW>& d, int lane, int wave) {
+  using D = KData2<P, NW>;
+#pragma unroll
+  for (int i = 0; i < D::UPW; i++) {
+    const int s = wave + i * NW;
+    if (s < D::ST) {
+#pragma unroll
+      for (int mt = 0; mt < D::T1; mt++) load_k4(K + (size_t)(s * D::T1 + mt) * 256, lane, d.q[i][mt]);
+    }
+  }
+}
+
 template <class P, int NW, bool CACHED>
-__device__ __forceinline__ void phase2_s2(_Float16* re, _Float16* im, const float2* __restrict__ K,
+__device__ __forceinline__ void phase2_s2(_Float16* re, _Float16* im, const KData2<P, NW>& kd,
                                           const h8* __restrict__ ftab, int acc16, int lane, int wave) {
   constexpr int R0 = P::R0, R1 = P::R1, N = P::N, ST = R0 / 16, T1 = R1 / 16;
   constexpr int UPW = (ST + NW - 1) / NW;
@@ -319,7 +366,7 @@ __device__ __forceinline__ void phase2_s2(_Float16* re, _Float16* im, const floa
         di[mt] = round_acc(di[mt], acc16);
       }
       h8 a2[T1];
-      spectrum_product<T1>(dr, di, K + (size_t)s * T1 * 256, lane, a2);
+      spectrum_product<T1>(dr, di, kd.q[i], a2);
 #pragma unroll
       for (int nt = 0; nt < T1; nt++) {
         f4 er = {0.f, 0.f, 0.f, 0.f}, ei = {0.f, 0.f, 0.f, 0.f};
@@ -374,6 +421,11 @@ __device__ __forceinline__ void phase2_s3(_Float16* re, _Float16* im, const floa
   for (int i = 0; i < ROWS; i++) {
     const int k0 = wave + i * NW;
     const int rb = k0 * P::ROW;
+    float4 kq[T1][T2][2];  // this row's spectrum, in flight while the stage over n1 runs
+#pragma unroll
+    for (int t1 = 0; t1 < T1; t1++)
+#pragma unroll
+      for (int mt = 0; mt < T2; mt++) load_k4(K + (size_t)((k0 * T1 + t1) * T2 + mt) * 256, lane, kq[t1][mt]);
     {  // stage over n1: [n2][n1] -> [k1][n2]
       h8 a[T2][T1];
 #pragma unroll
@@ -428,7 +480,7 @@ __device__ __forceinline__ void phase2_s3(_Float16* re, _Float16* im, const floa
           di[mt] = round_acc(di[mt], acc16);
         }
         h8 a2[T2];
-        spectrum_product<T2>(dr, di, K + (size_t)(k0 * T1 + t1) * T2 * 256, lane, a2);
+        spectrum_product<T2>(dr, di, kq[t1], a2);
 #pragma unroll
         for (int nt = 0; nt < T2; nt++) {
           f4 er = {0.f, 0.f, 0.f, 0.f}, ei = {0.f, 0.f, 0.f, 0.f};
@@ -565,9 +617,24 @@ __device__ __forceinline__ void phase3(TIO* __restrict__ ya, TIO* __restrict__ y
 }
 
 // ---- The fused kernel (src/sffft.cu:243-280) ------------------------------------
-// grid = H * (B / NSEQ) workgroups, batch index fastest (block -> (h, b) as in
-// src/sffft.cu:249) so the B/NSEQ workgroups of one channel run back to back and
-// share that channel's spectrum in cache.
+// Block -> (channel h, batch pair bp). The reference orders blocks batch-fastest
+// (src/sffft.cu:249) so one channel's spectrum is reused from cache. Workgroups are
+// dispatched to the 8 XCDs round-robin (block i -> XCD i mod 8), each XCD with its
+// own L2, so when H is a multiple of 8 the B/NSEQ workgroups of a channel are given
+// consecutive slots of one XCD: the spectrum of that channel is fetched into one L2.
+__device__ __forceinline__ void block_to_item(int i, int H, int BP, int& h, int& bp) {
+  if ((H & 7) == 0) {
+    const int x = i & 7, j = i >> 3, q = j / BP;
+    h = 8 * q + x;
+    bp = j - q * BP;
+  } else {
+    h = i / BP;
+    bp = i - h * BP;
+  }
+}
+
+// grid = H * (B / NSEQ) workgroups of 64*NW lanes; one sequence (NSEQ = 1) or one
+// pair of sequences of the same channel (NSEQ = 2) per workgroup.
 template <class P, int NW, int NSEQ, class TIO, bool CACHED>
 __global__ void __launch_bounds__(64 * NW)
     fftconv_kernel(const TIO* __restrict__ u, const float2* __restrict__ kf, TIO* __restrict__ y, int B, int H,
@@ -576,17 +643,26 @@ __global__ void __launch_bounds__(64 * NW)
   _Float16* re = lds;
   _Float16* im = lds + P::PLANE;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int BP = B / NSEQ;
-  const int h = blockIdx.x / BP, bp = blockIdx.x - h * BP;
+  int h, bp;
+  block_to_item(blockIdx.x, H, B / NSEQ, h, bp);
   const size_t row_a = ((size_t)(bp * NSEQ) * H + h) * P::L;
   const size_t row_b = NSEQ == 2 ? row_a + (size_t)H * P::L : row_a;
   const float2* K = kf + (size_t)h * P::N;
-  phase1<P, NW, NSEQ, TIO, CACHED>(u + row_a, u + row_b, re, im, ftab, acc16, lane, wave);
-  __syncthreads();
-  if constexpr (P::S == 2)
-    phase2_s2<P, NW, CACHED>(re, im, K, ftab, acc16, lane, wave);
-  else
+  // every global load of the input (and, for two-stage plans, of the spectrum) is
+  // issued before any computation, so their latencies overlap
+  P1Data<P, NW, NSEQ> ad;
+  p1_prefetch<P, NW, NSEQ, TIO>(u + row_a, u + row_b, ad, lane, wave);
+  if constexpr (P::S == 2) {
+    KData2<P, NW> kd;
+    k_prefetch_s2<P, NW>(K, kd, lane, wave);
+    phase1<P, NW, NSEQ, CACHED>(ad, re, im, ftab, acc16, lane, wave);
+    __syncthreads();
+    phase2_s2<P, NW, CACHED>(re, im, kd, ftab, acc16, lane, wave);
+  } else {
+    phase1<P, NW, NSEQ, CACHED>(ad, re, im, ftab, acc16, lane, wave);
+    __syncthreads();
     phase2_s3<P, NW, CACHED>(re, im, K, ftab, acc16, lane, wave);
+  }
   __syncthreads();
   phase3<P, NW, NSEQ, TIO, CACHED>(y + row_a, y + row_b, re, im, ftab, acc16, lane, wave);
 }
