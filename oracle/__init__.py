@@ -39,6 +39,8 @@ def lib() -> ctypes.CDLL:
         L.oracle_fft_conv.argtypes = [f32p, f32p, f64p, ci, ci, ci, ci]
         L.oracle_spectrum_p_order.argtypes = [f32p, ci, ci, ci, ci, f64p]
         L.oracle_fourstep_conv.argtypes = [f64p, f64p, ci, ci, ci, ci, ci, f64p]
+        L.oracle_round_f16.argtypes = [ctypes.c_double]
+        L.oracle_round_f16.restype = ctypes.c_double
         L.oracle_relative_l2.argtypes = [ctypes.c_double, ctypes.c_double]
         L.oracle_relative_l2.restype = ctypes.c_double
         _lib = L
@@ -112,6 +114,11 @@ def fourstep_conv(x, kf_p_order, r0, r1, r2=1, mode=0):
     y = np.empty(L, np.float64)
     lib().oracle_fourstep_conv(x, kf, L, r0, r1, r2, mode, y)
     return y
+
+
+def round_f16(x: float) -> float:
+    """IEEE binary16 round-to-nearest-even of a double (overflow to +-inf)."""
+    return lib().oracle_round_f16(x)
 
 
 def relative_l2(squared_error, squared_reference):

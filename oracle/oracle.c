@@ -243,6 +243,7 @@ static double round_f16(double x) {
   return nearbyint(x / q) * q; /* nearbyint: ties to even in the default rounding mode */
 }
 static double round_f32(double x) { return (double)(float)x; }
+double oracle_round_f16(double x) { return round_f16(x); }
 
 static int digit_stride(int J, int r1, int r2) { return J == 0 ? r1 * r2 : J == 1 ? r2 : 1; }
 static int twid_exp(int p, int J, int N, int r0, int r1, int r2) {

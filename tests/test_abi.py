@@ -1,0 +1,65 @@
+"""The C ABI of libsffft.so: every symbol declared in include/sffft.h is exported,
+and the host-side checks (plans, sizes, argument validation) behave without a GPU."""
+import ctypes
+import re
+
+import pytest
+
+import sffft_amd as sf
+
+
+def declared_functions():
+    text = open(sf.HEADER_PATH).read()
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?[a-z_0-9]+\s*\*?\s*(sffft_[a-z0-9_]+)\s*\(", text, re.M)))
+
+
+def test_every_declared_symbol_is_exported():
+    names = declared_functions()
+    assert len(names) >= 16
+    lib = ctypes.CDLL(sf.LIB_PATH)
+    for n in names:
+        assert hasattr(lib, n), n
+
+
+@pytest.mark.parametrize("L", sf.LENGTHS)
+def test_registry(L):
+    plans = sf.plans(L)
+    assert plans
+    for p in plans:
+        assert p.r0 * p.r1 * p.r2 == 2 * L
+        assert sf.plan_check(L, p) == sf.SFFFT_OK
+        assert sf.plan_check(L, p.replace(acc=1, cached=0)) == sf.SFFFT_OK
+        assert 0 < sf.lds_bytes(L, p) <= 163840
+    assert sf.plan_check(L, plans[0].replace(waves=3)) == sf.SFFFT_EINVAL
+
+
+def test_plan_validation():
+    P = sf.make_plan
+    assert sf.plan_check(1024, P("64x32", 4)) == sf.SFFFT_OK
+    assert sf.plan_check(1024, P("64x16", 4)) == sf.SFFFT_EINVAL       # product != 2L
+    assert sf.plan_check(1024, P("128x16", 4)) == sf.SFFFT_EINVAL      # radix 128
+    assert sf.plan_check(1000, P("64x32", 4)) == sf.SFFFT_EINVAL       # L not a power of two
+    assert sf.plan_check(1024, P("64x32", 4, seqs=3)) == sf.SFFFT_EINVAL
+    assert sf.plan_check(1024, P("64x32", 4, acc=2)) == sf.SFFFT_EINVAL
+    assert sf.plan_check(2048, P("16x16x16", 32)) == sf.SFFFT_EINVAL   # waves
+    assert sf.plan_check(1024, P("64x32", 1)) == sf.SFFFT_ENOPLAN      # valid, not compiled
+    assert sf.lds_bytes(1024, P("64x16", 4)) == 0
+
+
+def test_conv_argument_errors_need_no_gpu():
+    p = sf.make_plan("64x32", 4, seqs=2)
+    lib = sf.lib()
+    null = ctypes.c_void_p(0)
+    good = ctypes.c_void_p(1 << 20)
+    assert lib.sffft_conv_f32(null, good, good, 8, 768, 1024, ctypes.byref(p), null) == sf.SFFFT_EINVAL
+    assert lib.sffft_conv_f32(good, good, good, 7, 768, 1024, ctypes.byref(p), null) == sf.SFFFT_EINVAL  # B odd
+    assert lib.sffft_conv_f32(ctypes.c_void_p((1 << 20) + 4), good, good, 8, 768, 1024, ctypes.byref(p),
+                              null) == sf.SFFFT_EINVAL  # misaligned rows
+    assert lib.sffft_conv_bf16(good, good, good, 0, 768, 1024, ctypes.byref(p), null) == sf.SFFFT_EINVAL
+    assert lib.sffft_spectrum(good, 768, 1024, ctypes.byref(p), good, good, null) == sf.SFFFT_EINVAL  # kf == work
+    assert sf.lib().sffft_spectrum_bytes(768, 1024) == 768 * 2048 * 8
+
+
+def test_strerror():
+    assert sf.strerror(sf.SFFFT_OK) == "success"
+    assert "invalid" in sf.strerror(sf.SFFFT_EINVAL)

@@ -1,0 +1,112 @@
+"""GPU regression of the `sffft` driver, mirroring tests/precision_smoke.sh:36-86
+of the reference: unattainable targets, two seeds, fp16 overflow rejection,
+allocator modes and automatic legacy/cached selection."""
+import csv
+import io
+import math
+import os
+import subprocess
+
+import pytest
+
+import sffft_amd as sf
+
+pytestmark = pytest.mark.gpu
+NL = 7  # lengths 128..8192 of the default sweep
+
+
+def run(args, timeout=300):
+    print("cli:", " ".join(args), flush=True)
+    r = subprocess.run([sf.CLI_PATH] + args, capture_output=True, text=True, timeout=timeout)
+    rows = [row for row in csv.reader(io.StringIO(r.stdout)) if row and not row[0].startswith("#")]
+    return r.returncode, rows, r.stdout
+
+
+def num(x):
+    try:
+        return float(x)
+    except ValueError:
+        return math.nan
+
+
+def test_unattainable_targets(dev):
+    rc, rows, _ = run(["1", "1", "128", "--max-error", "1e-8", "--io", "fp32"])
+    assert rc == 2 and any(r[0] == "NO_MATCH" and r[1:3] == ["128", "fp32"] for r in rows)
+    rc, rows, _ = run(["1", "1", "128", "--max-error", "1e-3", "--io", "bf16"])
+    assert rc == 2 and any(r[0] == "NO_MATCH" and r[1:3] == ["128", "bf16"] for r in rows)
+
+
+@pytest.mark.parametrize("seed", ["42", "12345"])
+def test_two_seeds_select_every_length(dev, seed):
+    rc, rows, _ = run(["1", "1", "--max-error", "1e-3", "--io", "fp32", "--seed", seed])
+    sel = [r for r in rows if r[0] == "SELECT"]
+    assert rc == 0 and len(sel) == NL
+    assert all(num(r[5]) <= num(r[6]) and r[7] == "fp32" for r in sel)
+
+
+@pytest.mark.parametrize("kernel", ["legacy", "cached"])
+def test_fp16_overflow_rejected(dev, kernel):
+    rc, rows, _ = run(["1", "1", "128", "--max-error", "1e-3", "--io", "fp32", "--kernel", kernel,
+                       "--input-scale", "15000"])
+    rejected = [r for r in rows if r[0] == "RESULT" and "fp16acc" in r[2] and not math.isfinite(num(r[5]))]
+    sel = [r for r in rows if r[0] == "SELECT"]
+    assert rc == 0 and rejected and len(sel) == 1
+    assert sel[0][2] == "fused_fp32io" and num(sel[0][5]) <= num(sel[0][6])
+    rc, rows, _ = run(["1", "1", "128", "--max-error", "1e-3", "--io", "fp32", "--input-scale", "25000"])
+    assert rc == 2 and any(r[0] == "NO_MATCH" and r[1:3] == ["128", "fp32"] for r in rows)
+
+
+def _caps_ok(rows):
+    for r in rows:
+        if r[0] == "RESULT" and r[2].startswith("fused"):
+            e = num(r[5])
+            assert math.isfinite(e) and e <= (6e-3 if "bf16io" in r[2] else 2e-3), r
+
+
+@pytest.mark.parametrize("allocator", ["device", "managed", "mapped", "hybrid"])
+def test_allocators(dev, allocator):
+    _, rows, out = run(["--memory-info"])
+    caps = dict(kv.split("=") for kv in out.splitlines()[0].split(",")[1:])
+    rc, rows, _ = run(["1", "1", "--max-error", "1e-3", "--io", "fp32", "--allocator", allocator,
+                       "--kernel", "cached"])
+    if (allocator == "managed" and caps["managed"] == "0") or \
+            (allocator in ("mapped", "hybrid") and caps["mapped"] == "0"):
+        assert rc == 1  # unsupported allocators fail explicitly
+        return
+    assert rc == 0
+    _caps_ok(rows)
+    sel = [r for r in rows if r[0] == "SELECT"]
+    mem = [r for r in rows if r[0] == "MEMORY"]
+    assert len(sel) == NL and all("kernel_cached" in r[3] and r[7] == "fp32" and num(r[5]) <= num(r[6])
+                                  for r in sel)
+    assert len(mem) == NL
+    for r in mem:
+        assert r[2] == allocator
+        if allocator != "device":  # host-visible outputs: no downloads, no persistent shadows
+            assert num(r[7]) == 0 and num(r[4]) == 0
+        if allocator in ("managed", "mapped"):
+            assert num(r[6]) == 0
+
+
+@pytest.mark.parametrize("seed", ["42", "12345"])
+def test_auto_kernel_selection(dev, seed):
+    rc, rows, _ = run(["1", "1", "--max-error", "1e-3", "--io", "fp32", "--kernel", "auto", "--seed", seed])
+    assert rc == 0
+    _caps_ok(rows)
+    cached = sum(1 for r in rows if r[0] == "RESULT" and "kernel_cached" in r[3])
+    legacy = sum(1 for r in rows if r[0] == "RESULT" and "kernel_legacy" in r[3])
+    assert cached == legacy and cached > 0
+    assert sum(1 for r in rows if r[0] == "SELECT") == NL
+
+
+def test_full_size_rows_and_speedup(dev):
+    """B=8, H=768, L=1024: every fused candidate within the caps, and the selected
+    fp32 candidate at least 4x faster than the rocFFT pipeline."""
+    rc, rows, _ = run(["8", "768", "1024", "--kernel", "cached", "--max-error", "5e-4", "--io", "fp32"])
+    assert rc == 0
+    _caps_ok(rows)
+    pipe = [num(r[4]) for r in rows if r[0] == "RESULT" and r[2] == "rocfft_pipeline_fp32"][0]
+    ref_err = [num(r[5]) for r in rows if r[0] == "RESULT" and r[2] == "rocfft_pipeline_fp32"][0]
+    sel = [r for r in rows if r[0] == "SELECT"][0]
+    assert ref_err < 1e-6
+    assert num(sel[5]) <= 5e-4 and pipe / num(sel[4]) >= 4.0, (pipe, sel)
