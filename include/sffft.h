@@ -10,8 +10,8 @@
  *    u and y are [B][H][L] row-major; k is [H][L]; rows must be 16-byte aligned.
  *  - `stream` is a hipStream_t (NULL = default stream). Calls are asynchronous on
  *    that stream, reentrant, and allocate no memory, except that the first call on a
- *    device uploads an immutable 57,344-byte DFT coefficient table (kept for the
- *    life of the process).
+ *    device uploads an immutable 57,344-byte DFT coefficient table, and the first
+ *    mode-1 call of a plan its twiddle table (kept for the life of the process).
  *  - Every function returns SFFFT_OK (0) or a positive error code; nothing exits.
  */
 #ifndef SFFFT_H
@@ -36,8 +36,15 @@ extern "C" {
  *   acc   : 0 = fp32 accumulation, 1 = fp16 accumulation ("fp16acc" methods)
  *   cached: 1 = DFT matrices from the coefficient table ("kernel_cached"),
  *           0 = computed in the kernel ("kernel_legacy")  (src/sffft.cu:253-265)
- *   seqs  : sequences per workgroup: 1, or 2 (two batch rows of one channel packed
+ *   seqs  : sequences per transform: 1, or 2 (two batch rows of one channel packed
  *           as the real and imaginary parts of one complex transform; B must be even)
+ *   mode  : 0 = one workgroup per transform, stages exchanged through LDS;
+ *           1 = one wavefront per transform, stages chained in registers, `waves`
+ *               wavefronts per workgroup sharing LDS-resident DFT and twiddle tables
+ *               (two-stage plans, seqs = 2; the first call for such a plan on a device
+ *               uploads its immutable twiddle table, 16*L bytes)
+ *   channels : mode 1 only: channels per workgroup; their spectra are copied into
+ *           LDS once and shared by the wavefronts of each channel (mode 0: 1)
  */
 typedef struct sffft_plan {
   int r0, r1, r2;
@@ -45,6 +52,8 @@ typedef struct sffft_plan {
   int acc;
   int cached;
   int seqs;
+  int mode;
+  int channels;
 } sffft_plan;
 
 /* Plan validity: SFFFT_OK, SFFFT_EINVAL (bad radices/product/LDS), SFFFT_ENOPLAN.
@@ -59,8 +68,9 @@ size_t sffft_plan_lds_bytes(int L, const sffft_plan* plan);
 int sffft_plan_occupancy(int L, const sffft_plan* plan, int* blocks_per_cu);
 
 /* The plan registry used by the driver and the selector: the i-th compiled plan
- * for length L (acc = 0, cached = 1 are filled in; callers vary them). Writes the
- * plan name ("64x32") into name. Returns SFFFT_ENOTFOUND past the end.
+ * for length L (acc = 0, cached = 1 are filled in; callers vary them; r*, waves,
+ * seqs and mode identify the compiled kernel). Writes the plan name ("64x32") into
+ * name. Returns SFFFT_ENOTFOUND past the end.
  * Replaces the RUN(...) plan table (src/sffft.cu:506-513). */
 int sffft_plan_count(int L);
 int sffft_plan_get(int L, int index, sffft_plan* plan, char* name, size_t name_len);
@@ -69,6 +79,7 @@ int sffft_plan_get(int L, int index, sffft_plan* plan, char* name, size_t name_l
 size_t sffft_spectrum_bytes(int H, int L);
 
 /* Filter spectrum in the fused kernel's order, from the real filter k [H][L] fp32.
+ * The order depends on the radices and on the mode (mode 0 and mode 1 differ).
  * `work` must hold sffft_spectrum_bytes(H, L) bytes (scratch, clobbered).
  * Replaces: zero-pad + cufftExecC2C(FORWARD) + permuteK (src/sffft.cu:342-344,365,384,283-288).
  * Arithmetic: fp64 accumulation and twiddles, fp32 storage between the stages. */
@@ -79,7 +90,8 @@ int sffft_spectrum(const float* k, int H, int L, const sffft_plan* plan, void* k
  * Replaces permuteK (src/sffft.cu:283-288). kc and kf must not overlap. */
 int sffft_spectrum_from_natural(const void* kc, int H, int L, const sffft_plan* plan, void* kf, void* stream);
 
-/* The fused convolution, one launch: grid = H*B/seqs workgroups of 64*waves lanes.
+/* The fused convolution, one launch: grid = H*B/seqs workgroups of 64*waves lanes
+ * (mode 0) or ceil(H / channels) workgroups of 64*waves lanes (mode 1).
  * Replaces fftconv<P,W,float|bf16,TAcc,CACHED><<<B*H, 32*W, smem>>> (src/sffft.cu:243-280,389-390).
  * kf must come from sffft_spectrum* with the same L and the same r0/r1/r2. */
 int sffft_conv_f32(const float* u, const void* kf, float* y, int B, int H, int L, const sffft_plan* plan,

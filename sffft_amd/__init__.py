@@ -24,7 +24,9 @@ LENGTHS = (128, 256, 512, 1024, 2048, 4096, 8192, 16384)
 
 
 class Plan(ctypes.Structure):
-    """sffft_plan: N = 2L = r0*r1*r2 (r2 = 1 for two-stage plans)."""
+    """sffft_plan: N = 2L = r0*r1*r2 (r2 = 1 for two-stage plans). mode 0: one
+    workgroup per transform; mode 1: one wavefront per pair of sequences, `channels`
+    channels per workgroup."""
 
     _fields_ = [
         ("r0", ctypes.c_int),
@@ -34,6 +36,8 @@ class Plan(ctypes.Structure):
         ("acc", ctypes.c_int),
         ("cached", ctypes.c_int),
         ("seqs", ctypes.c_int),
+        ("mode", ctypes.c_int),
+        ("channels", ctypes.c_int),
     ]
 
     def name(self) -> str:
@@ -46,7 +50,7 @@ class Plan(ctypes.Structure):
 
     def __repr__(self) -> str:
         return (f"Plan({self.name()}, waves={self.waves}, acc={self.acc}, cached={self.cached}, "
-                f"seqs={self.seqs})")
+                f"seqs={self.seqs}, mode={self.mode}, channels={self.channels})")
 
 
 class Candidate(ctypes.Structure):
@@ -130,10 +134,11 @@ def plans(L: int) -> List[Plan]:
     return out
 
 
-def make_plan(spec: str, waves: int, acc: int = 0, cached: int = 1, seqs: int = 1) -> Plan:
+def make_plan(spec: str, waves: int, acc: int = 0, cached: int = 1, seqs: int = 1, mode: int = 0,
+              channels: int = 1) -> Plan:
     r = [int(x) for x in spec.split("x")]
     r += [1] * (3 - len(r))
-    return Plan(r[0], r[1], r[2], waves, acc, cached, seqs)
+    return Plan(r[0], r[1], r[2], waves, acc, cached, seqs, mode, channels)
 
 
 def plan_check(L: int, plan: Plan) -> int:

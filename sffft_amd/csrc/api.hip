@@ -6,11 +6,13 @@
 #include <cmath>
 #include <cstring>
 #include <limits>
+#include <map>
 #include <mutex>
 #include <vector>
 
 #include "../../include/sffft.h"
 #include "fftconv.hpp"
+#include "fftconv_wave.hpp"
 #include "registry.hpp"
 
 namespace sffft {
@@ -27,10 +29,18 @@ int hip_status(hipError_t err, const char* what) {
 
 bool valid_radix(int r) { return r == 16 || r == 32 || r == 64; }
 bool valid_length(int L) { return L >= 128 && L <= 16384 && (L & (L - 1)) == 0; }
-bool valid_waves(int w) { return w == 1 || w == 2 || w == 4 || w == 8 || w == 16; }
+// mode 0: 1, 2, 4, 8 or 16 wavefronts; mode 1 (one pair per wavefront): 1..16
+bool valid_waves(int w, int mode) {
+  return mode == 1 ? (w >= 1 && w <= 16) : (w == 1 || w == 2 || w == 4 || w == 8 || w == 16);
+}
 
-// Same formula as Plan<>::LDS_BYTES, for plans that are not compiled.
-size_t lds_bytes_rt(int r0, int r1, int r2) {
+// Same formulas as Plan<>::LDS_BYTES and WavePlan<>::LDS_BYTES, for plans that are
+// not compiled.
+size_t lds_bytes_rt(int r0, int r1, int r2, int mode, int channels) {
+  if (mode == 1) {
+    const int T0 = r0 / 16, T1 = r1 / 16;
+    return (size_t)(T0 * T0 * 128 + (r1 == r0 ? 0 : T1 * T1 * 128) + r0 * r1 + channels * r0 * r1 / 2) * 16;
+  }
   const int S = r2 > 1 ? 3 : 2, N = r0 * r1 * r2, M = N / r0;
   const int PA = r1 + LDS_PAD, PB = r0 + LDS_PAD, PC = r2 + LDS_PAD;
   const int ROW = S == 3 ? cmax(r2 * PA, r1 * PC) : 0;
@@ -56,11 +66,13 @@ int check_shape(int L, const sffft_plan* p) {
   if (!p || !valid_length(L)) return SFFFT_EINVAL;
   if (!valid_radix(p->r0) || !valid_radix(p->r1) || !(p->r2 == 1 || valid_radix(p->r2))) return SFFFT_EINVAL;
   if ((long long)p->r0 * p->r1 * p->r2 != 2LL * L) return SFFFT_EINVAL;
-  if (!valid_waves(p->waves) || (p->acc != 0 && p->acc != 1) || (p->cached != 0 && p->cached != 1) ||
-      (p->seqs != 1 && p->seqs != 2))
+  if (!valid_waves(p->waves, p->mode) || (p->acc != 0 && p->acc != 1) || (p->cached != 0 && p->cached != 1) ||
+      (p->seqs != 1 && p->seqs != 2) || (p->mode != 0 && p->mode != 1) || p->channels < 1 || p->channels > 16)
     return SFFFT_EINVAL;
-  if (p->r2 > 1 && p->r0 % p->waves) return SFFFT_EINVAL;
-  if (lds_bytes_rt(p->r0, p->r1, p->r2) > 163840) return SFFFT_EINVAL;
+  if (p->mode == 0 && p->channels != 1) return SFFFT_EINVAL;
+  if (p->mode == 1 && (p->r2 != 1 || p->seqs != 2)) return SFFFT_EINVAL;
+  if (p->mode == 0 && p->r2 > 1 && p->r0 % p->waves) return SFFFT_EINVAL;
+  if (lds_bytes_rt(p->r0, p->r1, p->r2, p->mode, p->channels) > 163840) return SFFFT_EINVAL;
   return SFFFT_OK;
 }
 
@@ -68,7 +80,8 @@ const Entry* find_entry(int L, const sffft_plan* p) {
   int n = 0;
   const Entry* e = entries_for(L, &n);
   for (int i = 0; i < n; i++)
-    if (e[i].r0 == p->r0 && e[i].r1 == p->r1 && e[i].r2 == p->r2 && e[i].waves == p->waves && e[i].seqs == p->seqs)
+    if (e[i].r0 == p->r0 && e[i].r1 == p->r1 && e[i].r2 == p->r2 && e[i].waves == p->waves &&
+        e[i].seqs == p->seqs && e[i].mode == p->mode && e[i].channels == p->channels)
       return &e[i];
   return nullptr;
 }
@@ -138,9 +151,79 @@ int device_table(const void** out) {
   return SFFFT_OK;
 }
 
+// ---- twiddle tables of the wave pipeline (fftconv_wave.hpp) ---------------------
+// TW1[tile mt*ST+nt][lane (c,g)][v] = sc0 * w^(m k0),        m = 16mt+4g+v, k0 = 16nt+c
+// TW2[tile s*MT+t][lane (c,g)][v]   = sc0 * sc1 * w^(k0 n1), k0 = 16s+4g+v,  n1 = 16t+c
+// with w = exp(-2 pi i / N), sc = 1/sqrt(R); exponents reduced mod N, fp64 then fp32.
+void build_twiddles(int r0, int r1, std::vector<float>& t) {
+  const int N = r0 * r1, ST = r0 / 16, MT = r1 / 16;
+  const double two_pi = 6.283185307179586476925286766559;
+  const double sc0 = 1.0 / std::sqrt((double)r0), sc1 = 1.0 / std::sqrt((double)r1);
+  t.assign((size_t)2 * N * 2, 0.f);
+  auto put = [&](size_t base, int tile, int lane, int v, long long e, double sc) {
+    e %= N;
+    if (e > N / 2) e -= N;
+    const double a = two_pi * (double)e / (double)N;
+    float* f = &t[base + ((size_t)tile * 64 + lane) * 8 + 2 * v];
+    f[0] = (float)(sc * std::cos(a));
+    f[1] = (float)(-sc * std::sin(a));
+  };
+  for (int mt = 0; mt < MT; mt++)
+    for (int nt = 0; nt < ST; nt++)
+      for (int lane = 0; lane < 64; lane++)
+        for (int v = 0; v < 4; v++) {
+          const int c = lane & 15, g = lane >> 4;
+          put(0, mt * ST + nt, lane, v, (long long)(16 * mt + 4 * g + v) * (16 * nt + c), sc0);
+        }
+  for (int s = 0; s < ST; s++)
+    for (int tt = 0; tt < MT; tt++)
+      for (int lane = 0; lane < 64; lane++)
+        for (int v = 0; v < 4; v++) {
+          const int c = lane & 15, g = lane >> 4;
+          put((size_t)2 * N, s * MT + tt, lane, v, (long long)(16 * s + 4 * g + v) * (16 * tt + c), sc0 * sc1);
+        }
+}
+
+std::mutex g_tw_mu;
+std::map<std::pair<int, int>, void*> g_tw[256];  // per device: (r0, r1) -> table
+
+int device_twiddles(int r0, int r1, const void** out) {
+  int dev = 0;
+  hipError_t err = hipGetDevice(&dev);
+  if (err != hipSuccess) return hip_status(err, "hipGetDevice");
+  if (dev < 0 || dev >= 256) return SFFFT_EINVAL;
+  std::lock_guard<std::mutex> lock(g_tw_mu);
+  void*& slot = g_tw[dev][std::make_pair(r0, r1)];
+  if (!slot) {
+    std::vector<float> host;
+    build_twiddles(r0, r1, host);
+    void* d = nullptr;
+    if ((err = hipMalloc(&d, host.size() * sizeof(float))) != hipSuccess) return hip_status(err, "hipMalloc");
+    if ((err = hipMemcpy(d, host.data(), host.size() * sizeof(float), hipMemcpyHostToDevice)) != hipSuccess) {
+      (void)hipFree(d);
+      return hip_status(err, "hipMemcpy");
+    }
+    slot = d;
+  }
+  *out = slot;
+  return SFFFT_OK;
+}
+
 // ---- filter spectrum ----------------------------------------------------------
-// Runtime form of kernel_order_digits<P>.
-__device__ inline void kernel_order_digits_rt(int idx, int r0, int r1, int r2, int& k0, int& k1, int& k2) {
+// Runtime form of kernel_order_digits<P> (mode 0) and of the wave pipeline's order
+// sp_index (mode 1: complex idx = 2*sp_index(s*MT + kt, lane, q) + e holds value
+// v = 2q + e of lane (c, g): k0 = 16s + c, k1 = 16kt + 4g + v).
+__device__ inline void kernel_order_digits_rt(int idx, int r0, int r1, int r2, int mode, int& k0, int& k1,
+                                              int& k2) {
+  if (mode == 1) {
+    const int e = idx & 1, lane = (idx >> 1) & 63, rest = idx >> 7;
+    const int q = rest & 1, tile = rest >> 1, MT = r1 / 16;
+    const int c = lane & 15, g = lane >> 4;
+    k0 = 16 * (tile / MT) + c;
+    k1 = 16 * (tile % MT) + 4 * g + 2 * q + e;
+    k2 = 0;
+    return;
+  }
   const int v = idx & 3, lane = (idx >> 2) & 63, rest = idx >> 8;
   const int c = lane & 15, g = lane >> 4;
   if (r2 == 1) {
@@ -213,13 +296,13 @@ __global__ void spectrum_stage_kernel(const float* __restrict__ k, float2* work,
 // Gather into the fused kernel's order, folding in 1/sqrt(R_last) of the last
 // forward stage. src is p-order (natural == 0) or natural frequency order.
 __global__ void spectrum_permute_kernel(const float2* __restrict__ src, float2* __restrict__ kf, int H, int r0,
-                                        int r1, int r2, int natural, float scale) {
+                                        int r1, int r2, int mode, int natural, float scale) {
   const int N = r0 * r1 * r2;
   const size_t gid = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (gid >= (size_t)H * N) return;
   const int h = (int)(gid / N), idx = (int)(gid % N);
   int k0, k1, k2;
-  kernel_order_digits_rt(idx, r0, r1, r2, k0, k1, k2);
+  kernel_order_digits_rt(idx, r0, r1, r2, mode, k0, k1, k2);
   const int s = natural ? k0 + r0 * k1 + r0 * r1 * k2 : k0 * (r1 * r2) + k1 * r2 + k2;
   const float2 v = src[(size_t)h * N + s];
   kf[gid] = make_float2(v.x * scale, v.y * scale);
@@ -248,7 +331,9 @@ int conv(const void* u, const void* kf, void* y, int B, int H, int L, const sfff
   if (!e) return SFFFT_ENOPLAN;
   const void* table = nullptr;
   if ((rc = device_table(&table))) return rc;
-  return hip_status(e->launch[IO][p->cached](u, kf, y, B, H, table, p->acc, (hipStream_t)stream),
+  const void* tw = nullptr;
+  if (e->mode == 1 && (rc = device_twiddles(p->r0, p->r1, &tw))) return rc;
+  return hip_status(e->launch[IO][p->cached](u, kf, y, B, H, table, tw, p->acc, (hipStream_t)stream),
                     "fused convolution launch");
 }
 
@@ -267,7 +352,7 @@ int sffft_plan_check(int L, const sffft_plan* plan) {
 
 size_t sffft_plan_lds_bytes(int L, const sffft_plan* plan) {
   if (check_shape(L, plan)) return 0;
-  return lds_bytes_rt(plan->r0, plan->r1, plan->r2);
+  return lds_bytes_rt(plan->r0, plan->r1, plan->r2, plan->mode, plan->channels);
 }
 
 int sffft_plan_occupancy(int L, const sffft_plan* plan, int* blocks_per_cu) {
@@ -300,6 +385,8 @@ int sffft_plan_get(int L, int index, sffft_plan* plan, char* name, size_t name_l
     plan->r2 = e[index].r2;
     plan->waves = e[index].waves;
     plan->seqs = e[index].seqs;
+    plan->mode = e[index].mode;
+    plan->channels = e[index].channels;
     plan->acc = 0;
     plan->cached = 1;
   }
@@ -334,7 +421,7 @@ int sffft_spectrum(const float* k, int H, int L, const sffft_plan* plan, void* k
   }
   const size_t total = (size_t)H * N;
   hipLaunchKernelGGL(spectrum_permute_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s,
-                     (const float2*)w, static_cast<float2*>(kf), H, plan->r0, plan->r1, plan->r2, 0,
+                     (const float2*)w, static_cast<float2*>(kf), H, plan->r0, plan->r1, plan->r2, plan->mode, 0,
                      last_stage_scale(plan));
   return hip_status(hipGetLastError(), "spectrum permute launch");
 }
@@ -346,7 +433,7 @@ int sffft_spectrum_from_natural(const void* kc, int H, int L, const sffft_plan* 
   const size_t total = (size_t)H * 2 * L;
   hipLaunchKernelGGL(spectrum_permute_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0,
                      (hipStream_t)stream, static_cast<const float2*>(kc), static_cast<float2*>(kf), H, plan->r0,
-                     plan->r1, plan->r2, 1, last_stage_scale(plan));
+                     plan->r1, plan->r2, plan->mode, 1, last_stage_scale(plan));
   return hip_status(hipGetLastError(), "spectrum permute launch");
 }
 

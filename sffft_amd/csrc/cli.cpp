@@ -11,7 +11,9 @@
 // prints RESULT,L,method,config,ms,rel_err lines; --max-error selects the fastest
 // candidate within the error budget (src/selection.h semantics via the C ABI).
 // Differences: L may also be 16384 (L=0 still sweeps 128..8192); "w" in the config
-// counts 64-lane wavefronts; the config ends with /seq<n> (rows per workgroup).
+// counts 64-lane wavefronts; the config ends with /seq<n> (rows per transform) and
+// /wg or /wave<c> (one workgroup per transform, or one wavefront per transform
+// with c channels per workgroup).
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -328,8 +330,13 @@ struct Bench {
       d += r * r;
     }
     char config[128];
-    snprintf(config, sizeof(config), "%s/w%d/occ%d/smem%zu/kernel_%s/seq%d", name, p.waves, occ, lds,
-             p.cached ? "cached" : "legacy", p.seqs);
+    char mode[16];
+    if (p.mode)
+      snprintf(mode, sizeof(mode), "wave%d", p.channels);
+    else
+      snprintf(mode, sizeof(mode), "wg");
+    snprintf(config, sizeof(config), "%s/w%d/occ%d/smem%zu/kernel_%s/seq%d/%s", name, p.waves, occ, lds,
+             p.cached ? "cached" : "legacy", p.seqs, mode);
     const char* m32 = p.acc ? "fused_fp16acc_fp32io" : "fused_fp32io";
     const char* m16 = p.acc ? "fused_fp16acc_bf16io" : "fused_bf16io";
     const double err32 = sffft_relative_l2(n1, d), err16 = sffft_relative_l2(n2, d);
@@ -343,14 +350,14 @@ struct Bench {
   // Every compiled plan for L, both accumulation types, legacy and/or cached DFT
   // matrices (src/sffft.cu:406-409, 507-513).
   void variants() {
-    std::tuple<int, int, int> spectrum_of = {0, 0, 0};
+    std::tuple<int, int, int, int> spectrum_of = {0, 0, 0, -1};
     const int n = sffft_plan_count(L);
     for (int i = 0; i < n; i++) {
       sffft_plan p;
       char name[32];
       SK(sffft_plan_get(L, i, &p, name, sizeof(name)));
       if (B % p.seqs) continue;
-      const std::tuple<int, int, int> radices = {p.r0, p.r1, p.r2};
+      const std::tuple<int, int, int, int> radices = {p.r0, p.r1, p.r2, p.mode};  // spectrum order
       if (radices != spectrum_of) {  // kernel-order spectrum from the rocFFT C2C spectrum (permuteK)
         SK(sffft_spectrum_from_natural(dkc, H, L, &p, dkf, nullptr));
         spectrum_of = radices;

@@ -1,6 +1,7 @@
-// Instantiates the fused kernel for every plan of one length (compiled once per
+// Instantiates the fused kernels for every plan of one length (compiled once per
 // length with -DSFFFT_INST_L=<L>, so the lengths build in parallel).
 #include "fftconv.hpp"
+#include "fftconv_wave.hpp"
 #include "registry.hpp"
 
 #ifndef SFFFT_INST_L
@@ -10,8 +11,8 @@
 namespace sffft {
 
 template <class P, int NW, int NSEQ, class TIO, bool CACHED>
-static hipError_t launch_fused(const void* u, const void* kf, void* y, int B, int H, const void* ftab, int acc16,
-                               hipStream_t stream) {
+static hipError_t launch_fused(const void* u, const void* kf, void* y, int B, int H, const void* ftab, const void*,
+                               int acc16, hipStream_t stream) {
   const unsigned grid = (unsigned)(H * (B / NSEQ));
   hipLaunchKernelGGL((fftconv_kernel<P, NW, NSEQ, TIO, CACHED>), dim3(grid), dim3(64 * NW), 0, stream,
                      static_cast<const TIO*>(u), static_cast<const float2*>(kf), static_cast<TIO*>(y), B, H,
@@ -19,23 +20,49 @@ static hipError_t launch_fused(const void* u, const void* kf, void* y, int B, in
   return hipGetLastError();
 }
 
-template <class P, int NW, int NSEQ, class TIO, bool CACHED>
-static const void* kernel_symbol() {
-  return reinterpret_cast<const void*>(&fftconv_kernel<P, NW, NSEQ, TIO, CACHED>);
+template <class P, int NW, int CH, class TIO, bool CACHED>
+static hipError_t launch_wave(const void* u, const void* kf, void* y, int B, int H, const void* ftab,
+                              const void* tw, int acc16, hipStream_t stream) {
+  const unsigned grid = (unsigned)((H + CH - 1) / CH);
+  if (acc16)
+    hipLaunchKernelGGL((fftconv_wave_kernel<P, NW, CH, TIO, CACHED, true>), dim3(grid), dim3(64 * NW), 0, stream,
+                       static_cast<const TIO*>(u), static_cast<const float4*>(kf), static_cast<TIO*>(y), B, H,
+                       static_cast<const h8*>(ftab), static_cast<const float4*>(tw));
+  else
+    hipLaunchKernelGGL((fftconv_wave_kernel<P, NW, CH, TIO, CACHED, false>), dim3(grid), dim3(64 * NW), 0, stream,
+                       static_cast<const TIO*>(u), static_cast<const float4*>(kf), static_cast<TIO*>(y), B, H,
+                       static_cast<const h8*>(ftab), static_cast<const float4*>(tw));
+  return hipGetLastError();
 }
 
 template <int A, int B_, int C_, int W, int S>
 static Entry make_entry() {
   typedef Plan<A, B_, C_> P;
-  Entry e = {SFFFT_INST_L, A, B_, C_, W, S, P::LDS_BYTES,
+  Entry e = {SFFFT_INST_L, A, B_, C_, W, S, 0, 1, P::LDS_BYTES,
              {{&launch_fused<P, W, S, float, false>, &launch_fused<P, W, S, float, true>},
               {&launch_fused<P, W, S, uint16_t, false>, &launch_fused<P, W, S, uint16_t, true>}},
-             {{kernel_symbol<P, W, S, float, false>(), kernel_symbol<P, W, S, float, true>()},
-              {kernel_symbol<P, W, S, uint16_t, false>(), kernel_symbol<P, W, S, uint16_t, true>()}}};
+             {{reinterpret_cast<const void*>(&fftconv_kernel<P, W, S, float, false>),
+               reinterpret_cast<const void*>(&fftconv_kernel<P, W, S, float, true>)},
+              {reinterpret_cast<const void*>(&fftconv_kernel<P, W, S, uint16_t, false>),
+               reinterpret_cast<const void*>(&fftconv_kernel<P, W, S, uint16_t, true>)}}};
+  return e;
+}
+
+template <int A, int B_, int W, int CH>
+static Entry make_wave_entry() {
+  typedef WavePlan<A, B_> P;
+  Entry e = {SFFFT_INST_L, A, B_, 1, W, 2, 1, CH, P::lds_bytes(CH),
+             {{&launch_wave<P, W, CH, float, false>, &launch_wave<P, W, CH, float, true>},
+              {&launch_wave<P, W, CH, uint16_t, false>, &launch_wave<P, W, CH, uint16_t, true>}},
+             {{reinterpret_cast<const void*>(&fftconv_wave_kernel<P, W, CH, float, false, false>),
+               reinterpret_cast<const void*>(&fftconv_wave_kernel<P, W, CH, float, true, false>)},
+              {reinterpret_cast<const void*>(&fftconv_wave_kernel<P, W, CH, uint16_t, false, false>),
+               reinterpret_cast<const void*>(&fftconv_wave_kernel<P, W, CH, uint16_t, true, false>)}}};
   return e;
 }
 
 #define SFFFT_PLAN(A, B_, C_, W) make_entry<A, B_, C_, W, 1>(), make_entry<A, B_, C_, W, 2>(),
+#define SFFFT_WAVE(A, B_, W, CH) make_wave_entry<A, B_, W, CH>(),
 
 static const Entry kEntries[] = {
 #include "plans.def"

@@ -1,0 +1,365 @@
+// Wave-pipeline fused causal long convolution for two-stage plans (N = R0*R1 = 2L).
+//
+// One 64-lane wavefront carries one pair of sequences of one channel -- packed as
+// the real and imaginary parts of a single complex transform -- through every
+// stage of the forward transform, the spectrum product and the inverse transform
+// without leaving VGPRs: no LDS transposes and no barriers between stages.
+//
+// Why it works (v_mfma_f32_16x16x32_f16, complex K interleave of fftconv.hpp):
+// a result tile D[i][j] sits in lane (j, g) as rows i = 4g..4g+3; an operand
+// fragment of the next contraction over i wants lane (j, g) to hold K indices
+// 4g..4g+3 for row/column j. They coincide, so each stage's accumulator tile,
+// twiddled and rounded to fp16, IS the next stage's operand with the roles of the
+// two indices swapped:
+//   phase 1  D1[m][k0]  = sum_{n0<R0/2} x[n0*M+m] F0[n0][k0]       (A = data, B = F0)
+//            B2[m][k0]  = fp16(D1 * sc0 * w^(m k0))                 -> B operand over m
+//   phase 2  D2[k1][k0] = sum_m F1[k1][m] B2[m][k0]                 (A = F1)
+//            A2[k0][k1] = fp16(conj(D2 * Kf))                       -> A operand over k1
+//            E[k0][n1]  = sum_k1 A2[k0][k1] F1[k1][n1]              (B = F1)
+//            A3[n1][k0] = fp16(E * sc1 * sc0 * w^(k0 n1))           -> A operand over k0
+//   phase 3  y_a[n0*M+m] =  Re sum_k0 A3[m][k0] F0[k0][n0],  y_b = -Im (n0 < R0/2)
+// which is the reference's schedule L0f -> Rf(x Kf) -> Ri -> L0i (src/sffft.cu:273-279)
+// with its digit order (src/sffft.cu:106-113, 283-288) and fp16 storage between
+// stages (src/sffft.cu:120-135); the inverse is computed as conj(DFT(conj X)).
+//
+// Read-only tables in LDS, filled once per workgroup:
+//   F0, F1 : DFT fragments of radix R0 and R1, both kinds ([cos | sin] and
+//            [-sin | cos]) in the order of the coefficient table
+//   TW1    : sc0 * w^(m k0) in the lane order of the phase-1 result tiles
+//   TW2    : sc1 * sc0 * w^(k0 n1) in the lane order of the inverse result tiles
+// so no twiddle is evaluated in the loop and no per-stage scale is applied; the
+// output scale 1/sqrt(R0) rides on TW2 and 1/sqrt(R1) on the spectrum.
+#pragma once
+#include "fftconv.hpp"
+
+namespace sffft {
+
+template <int R0_, int R1_>
+struct WavePlan {
+  static constexpr int R0 = R0_, R1 = R1_, N = R0 * R1, L = N / 2, M = R1;
+  static constexpr int MT = R1 / 16;                  // 16-wide tiles of m = n1 (and of k1)
+  static constexpr int ST = R0 / 16;                  // 16-wide strips of k0
+  static constexpr int KS1 = R0 >= 32 ? R0 / 32 : 1;  // phase-1 K steps (n0 < R0/2 only)
+  static constexpr int NT3 = R0 >= 32 ? R0 / 32 : 1;  // phase-3 result tiles (n0 < R0/2 only)
+  static constexpr int F0_H8 = ST * ST * 128;  // both fragment kinds
+  static constexpr int F1_H8 = R1 == R0 ? 0 : MT * MT * 128;
+  static constexpr int TW_F4 = N / 2;  // one twiddle table: N complex fp32 = N/2 float4
+  static constexpr int SP_F4 = N / 2;  // one channel's spectrum: N complex64 = N/2 float4
+  static constexpr int TAB_F4 = F0_H8 + F1_H8 + 2 * TW_F4;
+  // LDS of a workgroup holding `ch` channel spectra
+  static constexpr int lds_bytes(int ch) { return (TAB_F4 + ch * SP_F4) * 16; }
+  static_assert(R0 >= 16 && R0 <= 64 && R1 >= 16 && R1 <= 64, "radices are 16, 32 or 64");
+};
+
+// Twiddle-table index of lane `lane`, tile (a, b), float4 q (q = 0: values 0,1; q = 1: 2,3).
+__host__ __device__ constexpr int tw_index(int tile, int lane, int q) { return (tile * 64 + lane) * 2 + q; }
+// Spectrum index (float4 units) in the wave pipeline's order: tile = s*MT + kt,
+// q as above; lanes at 16-byte stride so one load instruction reads 1 KB.
+__host__ __device__ constexpr int sp_index(int tile, int lane, int q) { return (tile * 2 + q) * 64 + lane; }
+
+// DFT fragment (a, b, kind) of a radix-R table in LDS (coefficient-table order).
+template <int R>
+__device__ __forceinline__ h8 dft_frag(const h8* F, int a, int b, int kind, int lane) {
+  return F[((a * (R / 16) + b) * 2 + kind) * 64 + lane];
+}
+
+// (dr + i di) * w for four values, packed as an operand fragment [re | im] in fp16.
+__device__ __forceinline__ h8 cmul_pack(f4 dr, f4 di, float4 w01, float4 w23) {
+  const float wr[4] = {w01.x, w01.z, w23.x, w23.z};
+  const float wi[4] = {w01.y, w01.w, w23.y, w23.w};
+  h8 o;
+#pragma unroll
+  for (int v = 0; v < 4; v++) {
+    o[v] = (_Float16)(dr[v] * wr[v] - di[v] * wi[v]);
+    o[4 + v] = (_Float16)(dr[v] * wi[v] + di[v] * wr[v]);
+  }
+  return o;
+}
+
+// conj((dr + i di) * k) for four spectrum values k (float4 pairs of complex64).
+__device__ __forceinline__ h8 spectrum_conj_pack(f4 dr, f4 di, float4 k01, float4 k23) {
+  const float kr[4] = {k01.x, k01.z, k23.x, k23.z};
+  const float ki[4] = {k01.y, k01.w, k23.y, k23.w};
+  h8 o;
+#pragma unroll
+  for (int v = 0; v < 4; v++) {
+    o[v] = (_Float16)(dr[v] * kr[v] - di[v] * ki[v]);
+    o[4 + v] = (_Float16)(-(dr[v] * ki[v] + di[v] * kr[v]));
+  }
+  return o;
+}
+
+template <bool ACC16>
+__device__ __forceinline__ f4 acc_round(f4 v) {
+  if constexpr (ACC16) {
+#pragma unroll
+    for (int i = 0; i < 4; i++) v[i] = (float)(_Float16)v[i];
+  }
+  return v;
+}
+
+__device__ __forceinline__ float4 ld_f4(const float4* p) { return *p; }
+
+__device__ __forceinline__ void store4(float* p, f4 v) { *reinterpret_cast<float4*>(p) = make_float4(v[0], v[1], v[2], v[3]); }
+__device__ __forceinline__ void store4(uint16_t* p, f4 v) {
+  typedef float fl2 __attribute__((ext_vector_type(2)));
+  typedef __bf16 bf2 __attribute__((ext_vector_type(2)));
+  const bf2 lo = __builtin_convertvector((fl2){v[0], v[1]}, bf2);  // round to nearest even
+  const bf2 hi = __builtin_convertvector((fl2){v[2], v[3]}, bf2);
+  uint2 q;
+  q.x = __builtin_bit_cast(uint32_t, lo);
+  q.y = __builtin_bit_cast(uint32_t, hi);
+  *reinterpret_cast<uint2*>(p) = q;
+}
+
+// 16-byte blocks copied from global memory straight into LDS (global_load_lds_dwordx4:
+// lane i of the wave writes bytes [16i, 16i+16) after the wave-uniform LDS base).
+// `count` blocks, in runs of 64 per wave; the source of block k is src(k).
+template <int COUNT, int NW, class SRC>
+__device__ __forceinline__ void dma_to_lds(float4* dst, SRC src, int lane, int wave) {
+  static_assert(COUNT % 64 == 0, "tables are whole 64-block runs");
+  constexpr int RUNS = COUNT / 64;
+#pragma unroll
+  for (int i = 0; i < (RUNS + NW - 1) / NW; i++) {
+    const int run = i * NW + wave;
+    if (RUNS % NW == 0 || run < RUNS)
+      __builtin_amdgcn_global_load_lds(src(run * 64 + lane),
+                                       (__attribute__((address_space(3))) void*)(dst + run * 64), 16, 0, 0);
+  }
+}
+
+// DFT fragments of radix R (both kinds) computed into LDS (the in-kernel "legacy"
+// source), in coefficient-table order.
+template <int R, int NTH>
+__device__ __forceinline__ void compute_dft(h8* dst, int tid) {
+  constexpr int T = R / 16, TOTAL = T * T * 128;
+#pragma unroll
+  for (int i = 0; i < (TOTAL + NTH - 1) / NTH; i++) {
+    const int k = tid + i * NTH;
+    if (TOTAL % NTH == 0 || k < TOTAL) {
+      const int ab = k >> 7, kind = (k >> 6) & 1;
+      dst[k] = cf_frag<R, false>(nullptr, ab / T, ab % T, kind, k & 63);
+    }
+  }
+}
+
+// Global loads of one pair: the phase-1 operands of both rows.
+template <class P, class TIO>
+struct PairLoads {
+  TIO raw[P::MT][P::KS1][8];
+};
+
+template <class P, class TIO>
+__device__ __forceinline__ void issue_pair_loads(const TIO* __restrict__ xa, const TIO* __restrict__ xb,
+                                                 PairLoads<P, TIO>& d, int lane) {
+  constexpr int R0 = P::R0, M = P::M, MT = P::MT;
+  const int r = lane & 15, g = lane >> 4;
+  // lane bases at (n0 = 4g, m = r); every element is a constant offset from them
+  const TIO* pa = xa + (4 * g * M + r);
+  const TIO* pb = xb + (4 * g * M + r);
+  const bool live = R0 >= 32 || 4 * g < R0 / 2;  // R0 = 16: rows n0 >= 8 are the zero padding
+#pragma unroll
+  for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+    for (int ks = 0; ks < P::KS1; ks++)
+#pragma unroll
+      for (int j = 0; j < 8; j++) {
+        const int off = (16 * ks + (j & 3)) * M + 16 * mt;
+        d.raw[mt][ks][j] = live ? (j < 4 ? pa[off] : pb[off]) : (TIO)0;
+      }
+}
+
+// Every stage of one pair, from its loaded operands to the stored outputs; SP is the
+// channel's spectrum in LDS.
+template <class P, class TIO, bool ACC16, bool HOLD_F1>
+__device__ __forceinline__ void process_pair(const PairLoads<P, TIO>& d, const float4* SP, TIO* __restrict__ ya,
+                                             TIO* __restrict__ yb, const h8* F0, const h8* F1,
+                                             const float4* TW1, const float4* TW2, int lane) {
+  constexpr int R0 = P::R0, M = P::M, MT = P::MT, ST = P::ST, KS1 = P::KS1, NT3 = P::NT3;
+  const int r = lane & 15, g = lane >> 4;
+
+  // ---- phase 1: DFT over n0 (first R0/2 rows only), twiddle, -> B2[m tile][k0 strip]
+  h8 a[MT][KS1];
+#pragma unroll
+  for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+    for (int ks = 0; ks < KS1; ks++)
+#pragma unroll
+      for (int j = 0; j < 8; j++) a[mt][ks][j] = (_Float16)io_to_f32(d.raw[mt][ks][j]);
+  h8 b2[MT][ST];
+#pragma unroll
+  for (int nt = 0; nt < ST; nt++) {
+    h8 f0[KS1], f1[KS1];
+#pragma unroll
+    for (int ks = 0; ks < KS1; ks++) {
+      f0[ks] = dft_frag<R0>(F0, nt, ks, 0, lane);
+      f1[ks] = dft_frag<R0>(F0, nt, ks, 1, lane);
+    }
+#pragma unroll
+    for (int mt = 0; mt < MT; mt++) {
+      f4 dr = {0.f, 0.f, 0.f, 0.f}, di = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ks = 0; ks < KS1; ks++) {
+        dr = mfma(a[mt][ks], f0[ks], dr);
+        di = mfma(a[mt][ks], f1[ks], di);
+      }
+      dr = acc_round<ACC16>(dr);
+      di = acc_round<ACC16>(di);
+      const int t = mt * ST + nt;
+      b2[mt][nt] = cmul_pack(dr, di, TW1[tw_index(t, lane, 0)], TW1[tw_index(t, lane, 1)]);
+    }
+  }
+
+  // ---- phase 2: per k0 strip, DFT over n1, spectrum, inverse DFT over k1, twiddle
+  h8 g0[HOLD_F1 ? MT : 1][HOLD_F1 ? MT : 1][2];
+  if constexpr (HOLD_F1) {
+#pragma unroll
+    for (int i = 0; i < MT; i++)
+#pragma unroll
+      for (int k = 0; k < MT; k++)
+#pragma unroll
+        for (int kind = 0; kind < 2; kind++) g0[i][k][kind] = dft_frag<P::R1>(F1, i, k, kind, lane);
+  }
+  auto f1frag = [&](int i, int k, int kind) -> h8 {
+    if constexpr (HOLD_F1) return g0[i][k][kind];
+    else return dft_frag<P::R1>(F1, i, k, kind, lane);
+  };
+#pragma unroll
+  for (int s = 0; s < ST; s++) {
+    h8 a2[MT];
+#pragma unroll
+    for (int kt = 0; kt < MT; kt++) {
+      f4 dr = {0.f, 0.f, 0.f, 0.f}, di = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int mt = 0; mt < MT; mt++) {
+        dr = mfma(f1frag(kt, mt, 0), b2[mt][s], dr);
+        di = mfma(f1frag(kt, mt, 1), b2[mt][s], di);
+      }
+      dr = acc_round<ACC16>(dr);
+      di = acc_round<ACC16>(di);
+      const int tile = s * MT + kt;
+      a2[kt] = spectrum_conj_pack(dr, di, SP[sp_index(tile, lane, 0)], SP[sp_index(tile, lane, 1)]);
+    }
+#pragma unroll
+    for (int t = 0; t < MT; t++) {
+      f4 er = {0.f, 0.f, 0.f, 0.f}, ei = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int kt = 0; kt < MT; kt++) {
+        er = mfma(a2[kt], f1frag(t, kt, 0), er);
+        ei = mfma(a2[kt], f1frag(t, kt, 1), ei);
+      }
+      er = acc_round<ACC16>(er);
+      ei = acc_round<ACC16>(ei);
+      const int tt = s * MT + t;
+      b2[t][s] = cmul_pack(er, ei, TW2[tw_index(tt, lane, 0)], TW2[tw_index(tt, lane, 1)]);
+    }
+  }
+
+  // ---- phase 3: inverse DFT over k0 for n0 < R0/2; real part -> row a, -imag -> row b
+#pragma unroll
+  for (int nu = 0; nu < NT3; nu++) {
+    h8 f0[ST], f1[ST];
+#pragma unroll
+    for (int s = 0; s < ST; s++) {
+      f0[s] = dft_frag<R0>(F0, nu, s, 0, lane);
+      f1[s] = dft_frag<R0>(F0, nu, s, 1, lane);
+    }
+    const int n0 = 16 * nu + r;
+#pragma unroll
+    for (int t = 0; t < MT; t++) {
+      f4 za = {0.f, 0.f, 0.f, 0.f}, zb = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int s = 0; s < ST; s++) {
+        za = mfma(b2[t][s], f0[s], za);
+        zb = mfma(b2[t][s], f1[s], zb);
+      }
+      za = acc_round<ACC16>(za);
+      zb = -acc_round<ACC16>(zb);  // row b is minus the imaginary part
+      if (R0 >= 32 || n0 < R0 / 2) {
+        const int o = n0 * M + 16 * t + 4 * g;
+        store4(ya + o, za);
+        store4(yb + o, zb);
+      }
+    }
+  }
+}
+
+// grid = ceil(H / CH) workgroups of 64*NW lanes. Workgroup w takes channels
+// [w*CH, w*CH + CH) and their CH*(B/2) pairs, pair p = c*(B/2) + bp: rows (2bp, h)
+// and (2bp+1, h), h = w*CH + c. Wave v takes pairs v, v + NW, ... The DFT and
+// twiddle tables and the CH channel spectra are copied into LDS once, so the
+// B/2 wavefronts of a channel read its spectrum from LDS rather than each from L2.
+template <class P, int NW, int CH, class TIO, bool CACHED, bool ACC16>
+__global__ void __launch_bounds__(64 * NW)
+    fftconv_wave_kernel(const TIO* __restrict__ u, const float4* __restrict__ kf, TIO* __restrict__ y, int B,
+                        int H, const h8* __restrict__ ftab, const float4* __restrict__ twtab) {
+  constexpr int R0 = P::R0;
+  __shared__ float4 lds[P::TAB_F4 + CH * P::SP_F4];
+  h8* F0 = reinterpret_cast<h8*>(lds);
+  h8* F1 = P::R1 == P::R0 ? F0 : F0 + P::F0_H8;
+  float4* TW1 = lds + P::F0_H8 + P::F1_H8;
+  float4* TW2 = TW1 + P::TW_F4;
+  float4* SPL = lds + P::TAB_F4;
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int BP = B >> 1, h0 = blockIdx.x * CH;
+  const int nch = H - h0 < CH ? H - h0 : CH;  // channels of this workgroup
+
+  // ---- tables and spectra: direct global -> LDS copies, issued first
+  dma_to_lds<2 * P::TW_F4, NW>(TW1, [&](int k) { return twtab + k; }, lane, wave);
+  if constexpr (CACHED) {
+    dma_to_lds<P::F0_H8, NW>(reinterpret_cast<float4*>(F0), [&](int k) {
+      return reinterpret_cast<const float4*>(ftab + cf_off(R0) + k);
+    }, lane, wave);
+    if constexpr (P::R1 != P::R0)
+      dma_to_lds<P::F1_H8, NW>(reinterpret_cast<float4*>(F1), [&](int k) {
+        return reinterpret_cast<const float4*>(ftab + cf_off(P::R1) + k);
+      }, lane, wave);
+  }
+  {
+    // channel c of this workgroup is in slot c; slots past the last channel copy
+    // the last channel again (in bounds, never read)
+    const float4* src = kf + (size_t)h0 * P::SP_F4;
+    const int last = nch * P::SP_F4 - 1;
+    dma_to_lds<CH * P::SP_F4, NW>(SPL, [&](int k) { return src + (k < last ? k : last); }, lane, wave);
+  }
+
+  // ---- the first pair's loads. The waves of the first channel issue theirs
+  // before the table copies and the rest after the tables have landed, so the
+  // first channel's data arrives (and is computed and stored) while the other
+  // channels' data is still in flight.
+  const int npairs = nch * BP;
+  PairLoads<P, TIO> cur;
+  auto load_first = [&]() {
+    if (wave < npairs) {
+      const int c = wave / BP, bp = wave - c * BP;
+      const size_t ra = ((size_t)(2 * bp) * H + h0 + c) * P::L;
+      issue_pair_loads<P, TIO>(u + ra, u + ra + (size_t)H * P::L, cur, lane);
+    }
+  };
+  const bool early = wave < BP;
+  if (early) load_first();
+  if constexpr (!CACHED) {
+    compute_dft<R0, 64 * NW>(F0, tid);
+    if constexpr (P::R1 != P::R0) compute_dft<P::R1, 64 * NW>(F1, tid);
+  }
+  // the LDS copies count as vector-memory loads: wait for all of them (and for the
+  // early pair loads issued before them)
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (!early) load_first();
+
+  for (int p = wave; p < npairs; p += NW) {
+    // compiler-only barrier: keeps the table reads inside the loop (hoisting them
+    // would pin every twiddle tile in VGPRs)
+    __asm__ volatile("" ::: "memory");
+    const int c = p / BP, bp = p - c * BP;
+    const size_t ra = ((size_t)(2 * bp) * H + h0 + c) * P::L, rb = ra + (size_t)H * P::L;
+    if (p != wave) issue_pair_loads<P, TIO>(u + ra, u + rb, cur, lane);
+    // phase-2 fragments stay in VGPRs when the register budget allows (up to 8 waves
+    // per workgroup, at most two 16-wide tiles per radix-R1 axis)
+    process_pair<P, TIO, ACC16, (NW <= 8 && P::MT <= 2)>(cur, SPL + c * P::SP_F4, y + ra, y + rb, F0, F1, TW1, TW2, lane);
+  }
+}
+
+}  // namespace sffft

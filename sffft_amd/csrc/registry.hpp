@@ -4,13 +4,20 @@
 
 namespace sffft {
 
-typedef hipError_t (*launch_fn)(const void* u, const void* kf, void* y, int B, int H, const void* ftab, int acc16,
-                                hipStream_t stream);
+// Launches one instantiation. `tw` is the plan's twiddle table (wave pipeline only).
+typedef hipError_t (*launch_fn)(const void* u, const void* kf, void* y, int B, int H, const void* ftab,
+                                const void* tw, int acc16, hipStream_t stream);
 
-// One (plan, waves, sequences-per-workgroup) instantiation: launchers and kernel
+// One (plan, waves, sequences-per-workgroup, mode) instantiation: launchers and kernel
 // symbols for [io: 0 = fp32, 1 = bf16][cached: 0 = in-kernel DFT matrices, 1 = table].
+//   mode 0: one workgroup per sequence (seqs = 1) or pair of sequences (seqs = 2),
+//           stages exchanged through LDS (fftconv.hpp)
+//   mode 1: one wavefront per pair of sequences, stages chained in VGPRs; a workgroup
+//           of `waves` wavefronts takes `channels` channels and shares their spectra
+//           and the DFT and twiddle tables in LDS (fftconv_wave.hpp; two-stage
+//           plans, seqs = 2)
 struct Entry {
-  int L, r0, r1, r2, waves, seqs, lds_bytes;
+  int L, r0, r1, r2, waves, seqs, mode, channels, lds_bytes;
   launch_fn launch[2][2];
   const void* func[2][2];
 };

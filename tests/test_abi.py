@@ -30,7 +30,7 @@ def test_registry(L):
         assert sf.plan_check(L, p) == sf.SFFFT_OK
         assert sf.plan_check(L, p.replace(acc=1, cached=0)) == sf.SFFFT_OK
         assert 0 < sf.lds_bytes(L, p) <= 163840
-    assert sf.plan_check(L, plans[0].replace(waves=3)) == sf.SFFFT_EINVAL
+    assert sf.plan_check(L, plans[0].replace(waves=17)) == sf.SFFFT_EINVAL
 
 
 def test_plan_validation():
@@ -43,6 +43,13 @@ def test_plan_validation():
     assert sf.plan_check(1024, P("64x32", 4, acc=2)) == sf.SFFFT_EINVAL
     assert sf.plan_check(2048, P("16x16x16", 32)) == sf.SFFFT_EINVAL   # waves
     assert sf.plan_check(1024, P("64x32", 1)) == sf.SFFFT_ENOPLAN      # valid, not compiled
+    assert sf.plan_check(1024, P("64x32", 12, seqs=2, mode=1, channels=3)) == sf.SFFFT_OK
+    assert sf.plan_check(1024, P("64x32", 12)) == sf.SFFFT_EINVAL       # 12 waves: mode 1 only
+    assert sf.plan_check(1024, P("64x32", 12, seqs=1, mode=1, channels=3)) == sf.SFFFT_EINVAL  # pairs only
+    assert sf.plan_check(4096, P("32x16x16", 4, seqs=2, mode=1)) == sf.SFFFT_EINVAL  # two-stage only
+    assert sf.plan_check(1024, P("64x32", 4, channels=2)) == sf.SFFFT_EINVAL  # channels: mode 1 only
+    # LDS of a wave plan: tables (DFT fragments, two twiddle tables) + one spectrum per channel
+    assert sf.lds_bytes(1024, P("64x32", 12, seqs=2, mode=1, channels=3)) == (32768 + 8192 + 32768 + 3 * 16384)
     assert sf.lds_bytes(1024, P("64x16", 4)) == 0
 
 
