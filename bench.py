@@ -55,12 +55,31 @@ def parse():
     ap.add_argument("--rotate-mb", type=float, default=600.0,
                     help="minimum total size of the rotated buffer sets (0 = one warm set)")
     ap.add_argument("--cpu-baseline", type=int, default=1, help="time the fp64 CPU baseline (rank 0, N=1)")
-    ap.add_argument("--cpu-seconds", type=float, default=15.0, help="CPU sample budget")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU sample budget (seconds)")
     ap.add_argument("--check", type=int, default=1, help="verify the output against the fp64 oracle")
     ap.add_argument("--copy-mb", type=float, default=0.0,
                     help="instead of the convolution, time a plain device-to-device copy of this many MB "
                          "(bandwidth reference and the calibration run for HBM byte counters)")
     return ap.parse_args()
+
+
+def profiled_traffic(workload: str, plan) -> "int | None":
+    """HBM bytes per launch measured by rocprofv3 PMC runs (FETCH_SIZE, WRITE_SIZE,
+    calibrated on a plain copy) for this workload and plan, from the committed
+    summaries under profiles/ (their `workload:`, `plan:` and
+    `traffic_bytes_per_launch:` lines); None when no summary covers them."""
+    import glob
+    import re
+
+    want_plan = (f"plan: {plan.name()} waves={plan.waves} seqs={plan.seqs} mode={plan.mode} "
+                 f"channels={plan.channels}")
+    for path in sorted(glob.glob(os.path.join(ROOT, "profiles", "*.md"))):
+        text = open(path).read()
+        if f"workload: {workload}\n" in text and want_plan + "\n" in text:
+            m = re.search(r"^traffic_bytes_per_launch: (\d+)$", text, re.M)
+            if m:
+                return int(m.group(1))
+    return None
 
 
 def copy_reference(a):
@@ -210,6 +229,8 @@ def main():
     achieved = algo_bytes / (ms * 1e-3) / 1e9
 
     # ---- CPU baseline: the reference's fp64 direct convolution (oracle port) ----
+    # A bounded sample of the same workload: whole-batch passes repeated for about
+    # cpu_seconds when a pass is short, otherwise the first sequences of one pass.
     cpu = None
     if a.cpu_baseline:
         import oracle
@@ -218,21 +239,31 @@ def main():
         u, k = sets[0][4], sets[0][3]
         u_np = u.cpu().numpy()
         k_np = k.cpu().numpy()
-        # bounded sample: whole batch rows in (b,h) order, sized from a 1-sequence probe
         t1 = time.perf_counter()
         oracle.direct_conv(u_np[:1, :1], k_np[:1], nthreads=1)
         per_seq = max(time.perf_counter() - t1, 1e-6)
-        nseq = int(min(B * H, max(cores, a.cpu_seconds * cores / per_seq)))
-        nseq = max(cores, (nseq // cores) * cores) if nseq >= cores else nseq
-        us = u_np.reshape(B * H, L)[:nseq].reshape(1, nseq, L)
-        ks = np.stack([k_np[s % H] for s in range(nseq)])
-        t1 = time.perf_counter()
-        oracle.direct_conv(us, ks, nthreads=cores)
-        dt = time.perf_counter() - t1
-        cpu = {"value": dt * 1e3 * (B * H) / nseq, "unit": "ms per batch (scaled from sample)", "cores": cores,
-               "kind": "port",
-               "sample": f"fp64 direct convolution (src/sffft.cu:377 loop order) of {nseq} of {B * H} sequences "
-                         f"at L={L}, {dt:.2f} s on {cores} threads, scaled linearly to the batch"}
+        est_batch = per_seq * B * H / cores
+        if est_batch <= a.cpu_seconds:
+            reps, done = 0, 0.0
+            t1 = time.perf_counter()
+            while done < a.cpu_seconds or reps == 0:
+                oracle.direct_conv(u_np, k_np, nthreads=cores)
+                reps += 1
+                done = time.perf_counter() - t1
+            value = done * 1e3 / reps
+            sample = (f"fp64 direct convolution (src/sffft.cu:377 loop order) of the whole batch "
+                      f"({B * H} sequences at L={L}) repeated {reps} times, {done:.1f} s on {cores} threads")
+        else:
+            nseq = max(cores, int(a.cpu_seconds * cores / per_seq) // cores * cores)
+            us = u_np.reshape(B * H, L)[:nseq].reshape(1, nseq, L)
+            ks = np.stack([k_np[s_ % H] for s_ in range(nseq)])
+            t1 = time.perf_counter()
+            oracle.direct_conv(us, ks, nthreads=cores)
+            done = time.perf_counter() - t1
+            value = done * 1e3 * (B * H) / nseq
+            sample = (f"fp64 direct convolution (src/sffft.cu:377 loop order) of the first {nseq} of {B * H} "
+                      f"sequences at L={L}, {done:.1f} s on {cores} threads, scaled linearly to the batch")
+        cpu = {"value": round(value, 3), "unit": "ms per batch", "cores": cores, "kind": "port", "sample": sample}
 
     out = {
         "metric": "ms per B=8xH=768 batch vs L (fp32/bf16 I/O); % HBM roofline; rel L2 err",
@@ -254,7 +285,8 @@ def main():
                    "acc": "fp16" if plan.acc else "fp32", "rotated_sets": nsets,
                    "rotated_bytes": nsets * set_bytes},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None},
+                     "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "traffic": profiled_traffic(f"B={B} H={H} L={L} {io}", plan)},
         "cpu_baseline": cpu,
         "ms_warm": round(ms_warm, 6),
         "ms_eager": round(ms_eager, 6),

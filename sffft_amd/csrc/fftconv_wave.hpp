@@ -114,19 +114,51 @@ __device__ __forceinline__ void store4(uint16_t* p, f4 v) {
 
 // 16-byte blocks copied from global memory straight into LDS (global_load_lds_dwordx4:
 // lane i of the wave writes bytes [16i, 16i+16) after the wave-uniform LDS base).
-// `count` blocks, in runs of 64 per wave; the source of block k is src(k).
+// COUNT blocks in runs of 64, run r by wave r mod NW. Every wave issues exactly
+// dma_issues<COUNT, NW>() instructions (a wave without a run of its own in the last
+// round copies the last run again: same source, same bytes, same place), so the
+// caller knows how many vector-memory operations follow.
+template <int COUNT, int NW>
+__host__ __device__ constexpr int dma_issues() { return (COUNT / 64 + NW - 1) / NW; }
+
 template <int COUNT, int NW, class SRC>
 __device__ __forceinline__ void dma_to_lds(float4* dst, SRC src, int lane, int wave) {
   static_assert(COUNT % 64 == 0, "tables are whole 64-block runs");
   constexpr int RUNS = COUNT / 64;
 #pragma unroll
-  for (int i = 0; i < (RUNS + NW - 1) / NW; i++) {
-    const int run = i * NW + wave;
-    if (RUNS % NW == 0 || run < RUNS)
-      __builtin_amdgcn_global_load_lds(src(run * 64 + lane),
-                                       (__attribute__((address_space(3))) void*)(dst + run * 64), 16, 0, 0);
+  for (int i = 0; i < dma_issues<COUNT, NW>(); i++) {
+    int run = i * NW + wave;
+    if (RUNS % NW != 0 && run >= RUNS) run = RUNS - 1;
+    __builtin_amdgcn_global_load_lds(src(run * 64 + lane), (__attribute__((address_space(3))) void*)(dst + run * 64),
+                                     16, 0, 0);
   }
 }
+
+// Vector-memory instructions issue_pair_loads emits (one per operand slot).
+template <class P>
+__host__ __device__ constexpr int pair_load_issues() { return P::MT * P::KS1 * 8; }
+
+// s_waitcnt with the given vector-memory count and no wait on the other counters
+// (gfx9 encoding: vmcnt in bits 3:0 and 15:14, expcnt 6:4, lgkmcnt 11:8).
+// The count saturates at 63: with more operations in flight, waiting for 63 still
+// completes everything issued before the last 63 (the counter retires in order).
+template <int VM>
+__device__ __forceinline__ void wait_vmcnt() {
+  constexpr int V = VM > 63 ? 63 : VM;
+  static_assert(VM >= 0, "vmcnt is not negative");
+  __builtin_amdgcn_s_waitcnt((V & 15) | ((V >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+// 0 that the compiler cannot see through: adding it to the raw bits of the first
+// pair's operands keeps their conversion below the barrier (hoisted above it, the
+// conversion would make the wave wait for its loads before the barrier).
+__device__ __forceinline__ uint32_t opaque_zero() {
+  uint32_t v;
+  __asm__ volatile("v_mov_b32 %0, 0" : "=v"(v));
+  return v;
+}
+__device__ __forceinline__ float io_bits_to_f32(float x, uint32_t z) { return __uint_as_float(__float_as_uint(x) + z); }
+__device__ __forceinline__ float io_bits_to_f32(uint16_t x, uint32_t z) { return __uint_as_float(((uint32_t)x + z) << 16); }
 
 // DFT fragments of radix R (both kinds) computed into LDS (the in-kernel "legacy"
 // source), in coefficient-table order.
@@ -172,9 +204,9 @@ __device__ __forceinline__ void issue_pair_loads(const TIO* __restrict__ xa, con
 // Every stage of one pair, from its loaded operands to the stored outputs; SP is the
 // channel's spectrum in LDS.
 template <class P, class TIO, bool ACC16, bool HOLD_F1>
-__device__ __forceinline__ void process_pair(const PairLoads<P, TIO>& d, const float4* SP, TIO* __restrict__ ya,
-                                             TIO* __restrict__ yb, const h8* F0, const h8* F1,
-                                             const float4* TW1, const float4* TW2, int lane) {
+__device__ __forceinline__ void process_pair(const PairLoads<P, TIO>& d, uint32_t z, const float4* SP,
+                                             TIO* __restrict__ ya, TIO* __restrict__ yb, const h8* F0,
+                                             const h8* F1, const float4* TW1, const float4* TW2, int lane) {
   constexpr int R0 = P::R0, M = P::M, MT = P::MT, ST = P::ST, KS1 = P::KS1, NT3 = P::NT3;
   const int r = lane & 15, g = lane >> 4;
 
@@ -185,7 +217,7 @@ __device__ __forceinline__ void process_pair(const PairLoads<P, TIO>& d, const f
 #pragma unroll
     for (int ks = 0; ks < KS1; ks++)
 #pragma unroll
-      for (int j = 0; j < 8; j++) a[mt][ks][j] = (_Float16)io_to_f32(d.raw[mt][ks][j]);
+      for (int j = 0; j < 8; j++) a[mt][ks][j] = (_Float16)io_bits_to_f32(d.raw[mt][ks][j], z);
   h8 b2[MT][ST];
 #pragma unroll
   for (int nt = 0; nt < ST; nt++) {
@@ -323,42 +355,56 @@ __global__ void __launch_bounds__(64 * NW)
     const int last = nch * P::SP_F4 - 1;
     dma_to_lds<CH * P::SP_F4, NW>(SPL, [&](int k) { return src + (k < last ? k : last); }, lane, wave);
   }
-
-  // ---- the first pair's loads. The waves of the first channel issue theirs
-  // before the table copies and the rest after the tables have landed, so the
-  // first channel's data arrives (and is computed and stored) while the other
-  // channels' data is still in flight.
-  const int npairs = nch * BP;
-  PairLoads<P, TIO> cur;
-  auto load_first = [&]() {
-    if (wave < npairs) {
-      const int c = wave / BP, bp = wave - c * BP;
-      const size_t ra = ((size_t)(2 * bp) * H + h0 + c) * P::L;
-      issue_pair_loads<P, TIO>(u + ra, u + ra + (size_t)H * P::L, cur, lane);
-    }
-  };
-  const bool early = wave < BP;
-  if (early) load_first();
   if constexpr (!CACHED) {
     compute_dft<R0, 64 * NW>(F0, tid);
     if constexpr (P::R1 != P::R0) compute_dft<P::R1, 64 * NW>(F1, tid);
   }
-  // the LDS copies count as vector-memory loads: wait for all of them (and for the
-  // early pair loads issued before them)
-  __builtin_amdgcn_s_waitcnt(0);
-  __syncthreads();
-  if (!early) load_first();
 
-  for (int p = wave; p < npairs; p += NW) {
+  // ---- the first pairs. The waves of the first channel issue their loads right
+  // after the copies: they follow them in the vector-memory queue, so waiting for all
+  // but the last pair_load_issues() operations waits for the tables and spectra only
+  // and the pair's data stays in flight across the barrier (a __syncthreads() would
+  // drain it: its release fence waits for vmcnt 0). The other waves issue theirs
+  // after the barrier, so the first channel's data lands (and is computed and
+  // stored) while the rest is still in flight.
+  const int npairs = nch * BP;
+  PairLoads<P, TIO> cur;
+  auto issue_first = [&]() {
+    const int c = wave / BP, bp = wave - c * BP;
+    const size_t ra = ((size_t)(2 * bp) * H + h0 + c) * P::L;
+    issue_pair_loads<P, TIO>(u + ra, u + ra + (size_t)H * P::L, cur, lane);
+  };
+  const bool early = wave < BP && wave < npairs;
+  __asm__ volatile("" ::: "memory");
+  if (early) {
+    issue_first();
+    wait_vmcnt<pair_load_issues<P>()>();
+  } else {
+    wait_vmcnt<0>();
+  }
+  __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the in-kernel DFT fragments are written
+  __asm__ volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  __asm__ volatile("" ::: "memory");
+  if (!early && wave < npairs) issue_first();
+
+  // phase-2 fragments stay in VGPRs when the register budget allows (up to 8 waves
+  // per workgroup, at most two 16-wide tiles per radix-R1 axis)
+  constexpr bool HOLD = NW <= 8 && P::MT <= 2;
+  if (wave < npairs) {
+    const int c = wave / BP, bp = wave - c * BP;
+    const size_t ra = ((size_t)(2 * bp) * H + h0 + c) * P::L, rb = ra + (size_t)H * P::L;
+    process_pair<P, TIO, ACC16, HOLD>(cur, opaque_zero(), SPL + c * P::SP_F4, y + ra, y + rb, F0, F1, TW1, TW2,
+                                      lane);
+  }
+  for (int p = wave + NW; p < npairs; p += NW) {
     // compiler-only barrier: keeps the table reads inside the loop (hoisting them
     // would pin every twiddle tile in VGPRs)
     __asm__ volatile("" ::: "memory");
     const int c = p / BP, bp = p - c * BP;
     const size_t ra = ((size_t)(2 * bp) * H + h0 + c) * P::L, rb = ra + (size_t)H * P::L;
-    if (p != wave) issue_pair_loads<P, TIO>(u + ra, u + rb, cur, lane);
-    // phase-2 fragments stay in VGPRs when the register budget allows (up to 8 waves
-    // per workgroup, at most two 16-wide tiles per radix-R1 axis)
-    process_pair<P, TIO, ACC16, (NW <= 8 && P::MT <= 2)>(cur, SPL + c * P::SP_F4, y + ra, y + rb, F0, F1, TW1, TW2, lane);
+    issue_pair_loads<P, TIO>(u + ra, u + rb, cur, lane);
+    process_pair<P, TIO, ACC16, HOLD>(cur, 0u, SPL + c * P::SP_F4, y + ra, y + rb, F0, F1, TW1, TW2, lane);
   }
 }
 
