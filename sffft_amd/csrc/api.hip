@@ -36,10 +36,12 @@ bool valid_waves(int w, int mode) {
 
 // Same formulas as Plan<>::LDS_BYTES and WavePlan<>::LDS_BYTES, for plans that are
 // not compiled.
-size_t lds_bytes_rt(int r0, int r1, int r2, int mode, int channels) {
+size_t lds_bytes_rt(int r0, int r1, int r2, int mode, int channels, int waves) {
   if (mode == 1) {
     const int T0 = r0 / 16, T1 = r1 / 16;
-    return (size_t)(T0 * T0 * 128 + (r1 == r0 ? 0 : T1 * T1 * 128) + r0 * r1 + channels * r0 * r1 / 2) * 16;
+    // DFT fragments, two twiddle tables, the channel spectra, the per-wave operand scratch
+    return (size_t)(T0 * T0 * 128 + (r1 == r0 ? 0 : T1 * T1 * 128) + r0 * r1 + channels * r0 * r1 / 2) * 16 +
+           (size_t)waves * 16 * (r1 + 4) * 4;
   }
   const int S = r2 > 1 ? 3 : 2, N = r0 * r1 * r2, M = N / r0;
   const int PA = r1 + LDS_PAD, PB = r0 + LDS_PAD, PC = r2 + LDS_PAD;
@@ -72,7 +74,7 @@ int check_shape(int L, const sffft_plan* p) {
   if (p->mode == 0 && p->channels != 1) return SFFFT_EINVAL;
   if (p->mode == 1 && (p->r2 != 1 || p->seqs != 2)) return SFFFT_EINVAL;
   if (p->mode == 0 && p->r2 > 1 && p->r0 % p->waves) return SFFFT_EINVAL;
-  if (lds_bytes_rt(p->r0, p->r1, p->r2, p->mode, p->channels) > 163840) return SFFFT_EINVAL;
+  if (lds_bytes_rt(p->r0, p->r1, p->r2, p->mode, p->channels, p->waves) > 163840) return SFFFT_EINVAL;
   return SFFFT_OK;
 }
 
@@ -352,7 +354,7 @@ int sffft_plan_check(int L, const sffft_plan* plan) {
 
 size_t sffft_plan_lds_bytes(int L, const sffft_plan* plan) {
   if (check_shape(L, plan)) return 0;
-  return lds_bytes_rt(plan->r0, plan->r1, plan->r2, plan->mode, plan->channels);
+  return lds_bytes_rt(plan->r0, plan->r1, plan->r2, plan->mode, plan->channels, plan->waves);
 }
 
 int sffft_plan_occupancy(int L, const sffft_plan* plan, int* blocks_per_cu) {

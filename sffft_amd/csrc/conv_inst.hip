@@ -51,7 +51,7 @@ static Entry make_entry() {
 template <int A, int B_, int W, int CH>
 static Entry make_wave_entry() {
   typedef WavePlan<A, B_> P;
-  Entry e = {SFFFT_INST_L, A, B_, 1, W, 2, 1, CH, P::lds_bytes(CH),
+  Entry e = {SFFFT_INST_L, A, B_, 1, W, 2, 1, CH, P::lds_bytes(CH, W),
              {{&launch_wave<P, W, CH, float, false>, &launch_wave<P, W, CH, float, true>},
               {&launch_wave<P, W, CH, uint16_t, false>, &launch_wave<P, W, CH, uint16_t, true>}},
              {{reinterpret_cast<const void*>(&fftconv_wave_kernel<P, W, CH, float, false, false>),

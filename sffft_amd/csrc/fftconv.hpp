@@ -91,6 +91,15 @@ __device__ __forceinline__ uint16_t f32_to_bf16(float f) {
   x += 0x7fffu + ((x >> 16) & 1u);
   return (uint16_t)(x >> 16);
 }
+
+// Output stores carry the streaming (non-temporal) hint. Each output line is written
+// once and never read by the kernel; held dirty in the XCD's L2 it would be written
+// back by the end-of-kernel release, after the last wave, instead of during the run.
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ void stream_store(float* p, f4 v) { __builtin_nontemporal_store(v, reinterpret_cast<f4*>(p)); }
+__device__ __forceinline__ void stream_store(uint16_t* p, uint32_t lo, uint32_t hi) {
+  __builtin_nontemporal_store((u32x2){lo, hi}, reinterpret_cast<u32x2*>(p));
+}
 // fp16-accumulation mode: the raw tile accumulator is rounded to fp16 (range and
 // rounding of an fp16 accumulator; +-inf beyond 65504).
 __device__ __forceinline__ f4 round_acc(f4 v, int acc16) {
@@ -578,21 +587,18 @@ __device__ __forceinline__ void phase3(TIO* __restrict__ ya, TIO* __restrict__ y
     if (n0 < R0 / 2) {
       const int o = n0 * M + 16 * mt + 4 * g;
       if constexpr (sizeof(TIO) == 4) {
-        *reinterpret_cast<float4*>(ya + o) = make_float4(zr[0] * sc0, zr[1] * sc0, zr[2] * sc0, zr[3] * sc0);
-        if constexpr (NSEQ == 2)
-          *reinterpret_cast<float4*>(yb + o) =
-              make_float4(-zi[0] * sc0, -zi[1] * sc0, -zi[2] * sc0, -zi[3] * sc0);
+        stream_store(ya + o, zr * sc0);
+        if constexpr (NSEQ == 2) stream_store(yb + o, zi * -sc0);
       } else {
-        uint2 q;
-        q.x = (uint32_t)f32_to_bf16(zr[0] * sc0) | ((uint32_t)f32_to_bf16(zr[1] * sc0) << 16);
-        q.y = (uint32_t)f32_to_bf16(zr[2] * sc0) | ((uint32_t)f32_to_bf16(zr[3] * sc0) << 16);
-        *reinterpret_cast<uint2*>(ya + o) = q;
-        if constexpr (NSEQ == 2) {
-          q.x = (uint32_t)f32_to_bf16(-zi[0] * sc0) | ((uint32_t)f32_to_bf16(-zi[1] * sc0) << 16);
-          q.y = (uint32_t)f32_to_bf16(-zi[2] * sc0) | ((uint32_t)f32_to_bf16(-zi[3] * sc0) << 16);
-          *reinterpret_cast<uint2*>(yb + o) = q;
-        }
+        stream_store(ya + o, (uint32_t)f32_to_bf16(zr[0] * sc0) | ((uint32_t)f32_to_bf16(zr[1] * sc0) << 16),
+                     (uint32_t)f32_to_bf16(zr[2] * sc0) | ((uint32_t)f32_to_bf16(zr[3] * sc0) << 16));
+        if constexpr (NSEQ == 2)
+          stream_store(yb + o, (uint32_t)f32_to_bf16(-zi[0] * sc0) | ((uint32_t)f32_to_bf16(-zi[1] * sc0) << 16),
+                       (uint32_t)f32_to_bf16(-zi[2] * sc0) | ((uint32_t)f32_to_bf16(-zi[3] * sc0) << 16));
       }
+      // compiler-only barrier: loop store promotion would re-create the stores
+      // without their non-temporal hint
+      __asm__ volatile("" ::: "memory");
     }
   };
   auto load = [&](int mt, h8* a) {

@@ -46,8 +46,9 @@ struct WavePlan {
   static constexpr int TW_F4 = N / 2;  // one twiddle table: N complex fp32 = N/2 float4
   static constexpr int SP_F4 = N / 2;  // one channel's spectrum: N complex64 = N/2 float4
   static constexpr int TAB_F4 = F0_H8 + F1_H8 + 2 * TW_F4;
-  // LDS of a workgroup holding `ch` channel spectra
-  static constexpr int lds_bytes(int ch) { return (TAB_F4 + ch * SP_F4) * 16; }
+  // LDS of a workgroup of nw wavefronts holding `ch` channel spectra, with the
+  // per-wavefront operand scratch of fp32 I/O (bf16 needs less)
+  static constexpr int lds_bytes(int ch, int nw) { return (TAB_F4 + ch * SP_F4) * 16 + nw * 16 * (M + 4) * 4; }
   static_assert(R0 >= 16 && R0 <= 64 && R1 >= 16 && R1 <= 64, "radices are 16, 32 or 64");
 };
 
@@ -100,16 +101,13 @@ __device__ __forceinline__ f4 acc_round(f4 v) {
 
 __device__ __forceinline__ float4 ld_f4(const float4* p) { return *p; }
 
-__device__ __forceinline__ void store4(float* p, f4 v) { *reinterpret_cast<float4*>(p) = make_float4(v[0], v[1], v[2], v[3]); }
+__device__ __forceinline__ void store4(float* p, f4 v) { stream_store(p, v); }
 __device__ __forceinline__ void store4(uint16_t* p, f4 v) {
   typedef float fl2 __attribute__((ext_vector_type(2)));
   typedef __bf16 bf2 __attribute__((ext_vector_type(2)));
   const bf2 lo = __builtin_convertvector((fl2){v[0], v[1]}, bf2);  // round to nearest even
   const bf2 hi = __builtin_convertvector((fl2){v[2], v[3]}, bf2);
-  uint2 q;
-  q.x = __builtin_bit_cast(uint32_t, lo);
-  q.y = __builtin_bit_cast(uint32_t, hi);
-  *reinterpret_cast<uint2*>(p) = q;
+  stream_store(p, __builtin_bit_cast(uint32_t, lo), __builtin_bit_cast(uint32_t, hi));
 }
 
 // 16-byte blocks copied from global memory straight into LDS (global_load_lds_dwordx4:
@@ -134,10 +132,6 @@ __device__ __forceinline__ void dma_to_lds(float4* dst, SRC src, int lane, int w
   }
 }
 
-// Vector-memory instructions issue_pair_loads emits (one per operand slot).
-template <class P>
-__host__ __device__ constexpr int pair_load_issues() { return P::MT * P::KS1 * 8; }
-
 // s_waitcnt with the given vector-memory count and no wait on the other counters
 // (gfx9 encoding: vmcnt in bits 3:0 and 15:14, expcnt 6:4, lgkmcnt 11:8).
 // The count saturates at 63: with more operations in flight, waiting for 63 still
@@ -148,17 +142,6 @@ __device__ __forceinline__ void wait_vmcnt() {
   static_assert(VM >= 0, "vmcnt is not negative");
   __builtin_amdgcn_s_waitcnt((V & 15) | ((V >> 4) << 14) | (7 << 4) | (15 << 8));
 }
-
-// 0 that the compiler cannot see through: adding it to the raw bits of the first
-// pair's operands keeps their conversion below the barrier (hoisted above it, the
-// conversion would make the wave wait for its loads before the barrier).
-__device__ __forceinline__ uint32_t opaque_zero() {
-  uint32_t v;
-  __asm__ volatile("v_mov_b32 %0, 0" : "=v"(v));
-  return v;
-}
-__device__ __forceinline__ float io_bits_to_f32(float x, uint32_t z) { return __uint_as_float(__float_as_uint(x) + z); }
-__device__ __forceinline__ float io_bits_to_f32(uint16_t x, uint32_t z) { return __uint_as_float(((uint32_t)x + z) << 16); }
 
 // DFT fragments of radix R (both kinds) computed into LDS (the in-kernel "legacy"
 // source), in coefficient-table order.
@@ -175,36 +158,95 @@ __device__ __forceinline__ void compute_dft(h8* dst, int tid) {
   }
 }
 
-// Global loads of one pair: the phase-1 operands of both rows.
+// Global loads of one pair. The first L samples of a row are the non-zero half of
+// its length-2L transform input and are contiguous, so both rows are read as 16-byte
+// chunks, one KB per instruction, with the streaming (non-temporal) hint: chunk q of
+// the pair (rows a then b) goes to lane q % 64 of round q / 64.
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
 template <class P, class TIO>
 struct PairLoads {
-  TIO raw[P::MT][P::KS1][8];
+  static constexpr int EPC = 16 / (int)sizeof(TIO);  // samples per chunk
+  static constexpr int CPS = P::L / EPC;              // chunks per row
+  static constexpr int ROUNDS = (2 * CPS + 63) / 64;  // load instructions per pair
+  u32x4 c[ROUNDS];
 };
+
+// Vector-memory instructions issue_pair_loads emits.
+template <class P, class TIO>
+__host__ __device__ constexpr int pair_load_issues() { return PairLoads<P, TIO>::ROUNDS; }
 
 template <class P, class TIO>
 __device__ __forceinline__ void issue_pair_loads(const TIO* __restrict__ xa, const TIO* __restrict__ xb,
                                                  PairLoads<P, TIO>& d, int lane) {
-  constexpr int R0 = P::R0, M = P::M, MT = P::MT;
+  typedef PairLoads<P, TIO> D;
+#pragma unroll
+  for (int i = 0; i < D::ROUNDS; i++) {
+    const int q = i * 64 + lane;
+    if (2 * D::CPS >= (i + 1) * 64 || q < 2 * D::CPS) {
+      const TIO* row = q < D::CPS ? xa : xb;
+      const int off = q < D::CPS ? q : q - D::CPS;
+      d.c[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(row) + off);
+    }
+  }
+}
+
+// Per-wavefront LDS scratch that turns the row chunks into phase-1 operands: 16 rows
+// (one K step of n0) of M samples at a pitch chosen so that the four K groups of a
+// wavefront read four disjoint 16-bank ranges and every row start stays 16-byte aligned.
+template <class P, class TIO>
+__host__ __device__ constexpr int scratch_pitch() { return P::M + (sizeof(TIO) == 4 ? 4 : 8); }
+template <class P, class TIO>
+__host__ __device__ constexpr int scratch_bytes() { return 16 * scratch_pitch<P, TIO>() * (int)sizeof(TIO); }
+
+__device__ __forceinline__ float io_to_f32_lds(const float* p) { return *p; }
+__device__ __forceinline__ float io_to_f32_lds(const uint16_t* p) { return __uint_as_float((uint32_t)*p << 16); }
+
+// Phase-1 A operands a[mt][ks] (slots 0..3 row a, 4..7 row b; n0 = 16ks + 4g + j,
+// m = 16mt + r) from the pair's chunks, through the wave's scratch S.
+template <class P, class TIO>
+__device__ __forceinline__ void pair_operands(const PairLoads<P, TIO>& d, TIO* S, h8 (*a)[P::KS1], int lane) {
+  typedef PairLoads<P, TIO> D;
+  constexpr int R0 = P::R0, M = P::M, PITCH = scratch_pitch<P, TIO>();
+  constexpr int ROWS = R0 / 2 < 16 ? R0 / 2 : 16;  // non-zero rows per K step
   const int r = lane & 15, g = lane >> 4;
-  // lane bases at (n0 = 4g, m = r); every element is a constant offset from them
-  const TIO* pa = xa + (4 * g * M + r);
-  const TIO* pb = xb + (4 * g * M + r);
-  const bool live = R0 >= 32 || 4 * g < R0 / 2;  // R0 = 16: rows n0 >= 8 are the zero padding
 #pragma unroll
-  for (int mt = 0; mt < MT; mt++)
+  for (int ks = 0; ks < P::KS1; ks++)
 #pragma unroll
-    for (int ks = 0; ks < P::KS1; ks++)
+    for (int sq = 0; sq < 2; sq++) {
+      // chunks of rows [16ks, 16ks + ROWS) of row sq
+      constexpr int PER = ROWS * M / D::EPC;
+      const int lo = sq * D::CPS + ks * (16 * M / D::EPC);
 #pragma unroll
-      for (int j = 0; j < 8; j++) {
-        const int off = (16 * ks + (j & 3)) * M + 16 * mt;
-        d.raw[mt][ks][j] = live ? (j < 4 ? pa[off] : pb[off]) : (TIO)0;
+      for (int i = 0; i < D::ROUNDS; i++) {
+        const int q = i * 64 + lane;
+        if (q >= lo && q < lo + PER) {
+          const int e = (q - lo) * D::EPC;
+          *reinterpret_cast<u32x4*>(S + (e / M) * PITCH + e % M) = d.c[i];
+        }
       }
+      // A lane reads what other lanes wrote. The wavefront's LDS operations complete
+      // in order, so no instruction is needed, but the compiler models each lane
+      // alone: without these compiler-only barriers a lane that wrote nothing here
+      // would reuse its reads of the previous block, and writes could be moved above
+      // the previous block's reads.
+      __asm__ volatile("" ::: "memory");
+#pragma unroll
+      for (int mt = 0; mt < P::MT; mt++)
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+          const bool live = 4 * g + j < ROWS;
+          const float v = live ? io_to_f32_lds(S + (4 * g + j) * PITCH + 16 * mt + r) : 0.f;
+          a[mt][ks][4 * sq + j] = (_Float16)v;
+        }
+      __asm__ volatile("" ::: "memory");
+    }
 }
 
 // Every stage of one pair, from its loaded operands to the stored outputs; SP is the
 // channel's spectrum in LDS.
 template <class P, class TIO, bool ACC16, bool HOLD_F1>
-__device__ __forceinline__ void process_pair(const PairLoads<P, TIO>& d, uint32_t z, const float4* SP,
+__device__ __forceinline__ void process_pair(const PairLoads<P, TIO>& d, TIO* S, const float4* SP,
                                              TIO* __restrict__ ya, TIO* __restrict__ yb, const h8* F0,
                                              const h8* F1, const float4* TW1, const float4* TW2, int lane) {
   constexpr int R0 = P::R0, M = P::M, MT = P::MT, ST = P::ST, KS1 = P::KS1, NT3 = P::NT3;
@@ -212,12 +254,7 @@ __device__ __forceinline__ void process_pair(const PairLoads<P, TIO>& d, uint32_
 
   // ---- phase 1: DFT over n0 (first R0/2 rows only), twiddle, -> B2[m tile][k0 strip]
   h8 a[MT][KS1];
-#pragma unroll
-  for (int mt = 0; mt < MT; mt++)
-#pragma unroll
-    for (int ks = 0; ks < KS1; ks++)
-#pragma unroll
-      for (int j = 0; j < 8; j++) a[mt][ks][j] = (_Float16)io_bits_to_f32(d.raw[mt][ks][j], z);
+  pair_operands<P, TIO>(d, S, a, lane);
   h8 b2[MT][ST];
 #pragma unroll
   for (int nt = 0; nt < ST; nt++) {
@@ -312,6 +349,11 @@ __device__ __forceinline__ void process_pair(const PairLoads<P, TIO>& d, uint32_
         store4(ya + o, za);
         store4(yb + o, zb);
       }
+      // With one tile per axis (MT == 1) the loop runs once and the store addresses
+      // are loop-invariant: loop store promotion would re-create the stores without
+      // their non-temporal hint. A compiler-only barrier prevents that (with MT > 1
+      // it would only constrain scheduling).
+      if constexpr (MT == 1) __asm__ volatile("" ::: "memory");
     }
   }
 }
@@ -326,7 +368,8 @@ __global__ void __launch_bounds__(64 * NW)
     fftconv_wave_kernel(const TIO* __restrict__ u, const float4* __restrict__ kf, TIO* __restrict__ y, int B,
                         int H, const h8* __restrict__ ftab, const float4* __restrict__ twtab) {
   constexpr int R0 = P::R0;
-  __shared__ float4 lds[P::TAB_F4 + CH * P::SP_F4];
+  constexpr int SCR_F4 = scratch_bytes<P, TIO>() / 16;
+  __shared__ float4 lds[P::TAB_F4 + CH * P::SP_F4 + NW * SCR_F4];
   h8* F0 = reinterpret_cast<h8*>(lds);
   h8* F1 = P::R1 == P::R0 ? F0 : F0 + P::F0_H8;
   float4* TW1 = lds + P::F0_H8 + P::F1_H8;
@@ -334,6 +377,7 @@ __global__ void __launch_bounds__(64 * NW)
   float4* SPL = lds + P::TAB_F4;
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  TIO* S = reinterpret_cast<TIO*>(lds + P::TAB_F4 + CH * P::SP_F4 + wave * SCR_F4);
   const int BP = B >> 1, h0 = blockIdx.x * CH;
   const int nch = H - h0 < CH ? H - h0 : CH;  // channels of this workgroup
 
@@ -378,7 +422,7 @@ __global__ void __launch_bounds__(64 * NW)
   __asm__ volatile("" ::: "memory");
   if (early) {
     issue_first();
-    wait_vmcnt<pair_load_issues<P>()>();
+    wait_vmcnt<pair_load_issues<P, TIO>()>();
   } else {
     wait_vmcnt<0>();
   }
@@ -394,7 +438,7 @@ __global__ void __launch_bounds__(64 * NW)
   if (wave < npairs) {
     const int c = wave / BP, bp = wave - c * BP;
     const size_t ra = ((size_t)(2 * bp) * H + h0 + c) * P::L, rb = ra + (size_t)H * P::L;
-    process_pair<P, TIO, ACC16, HOLD>(cur, opaque_zero(), SPL + c * P::SP_F4, y + ra, y + rb, F0, F1, TW1, TW2,
+    process_pair<P, TIO, ACC16, HOLD>(cur, S, SPL + c * P::SP_F4, y + ra, y + rb, F0, F1, TW1, TW2,
                                       lane);
   }
   for (int p = wave + NW; p < npairs; p += NW) {
@@ -404,7 +448,7 @@ __global__ void __launch_bounds__(64 * NW)
     const int c = p / BP, bp = p - c * BP;
     const size_t ra = ((size_t)(2 * bp) * H + h0 + c) * P::L, rb = ra + (size_t)H * P::L;
     issue_pair_loads<P, TIO>(u + ra, u + rb, cur, lane);
-    process_pair<P, TIO, ACC16, HOLD>(cur, 0u, SPL + c * P::SP_F4, y + ra, y + rb, F0, F1, TW1, TW2, lane);
+    process_pair<P, TIO, ACC16, HOLD>(cur, S, SPL + c * P::SP_F4, y + ra, y + rb, F0, F1, TW1, TW2, lane);
   }
 }
 

@@ -49,7 +49,9 @@ def test_plan_validation():
     assert sf.plan_check(4096, P("32x16x16", 4, seqs=2, mode=1)) == sf.SFFFT_EINVAL  # two-stage only
     assert sf.plan_check(1024, P("64x32", 4, channels=2)) == sf.SFFFT_EINVAL  # channels: mode 1 only
     # LDS of a wave plan: tables (DFT fragments, two twiddle tables) + one spectrum per channel
-    assert sf.lds_bytes(1024, P("64x32", 12, seqs=2, mode=1, channels=3)) == (32768 + 8192 + 32768 + 3 * 16384)
+    # + a 16-row operand scratch per wavefront
+    assert sf.lds_bytes(1024, P("64x32", 12, seqs=2, mode=1, channels=3)) == (32768 + 8192 + 32768 + 3 * 16384 +
+                                                                            12 * 16 * 36 * 4)
     assert sf.lds_bytes(1024, P("64x16", 4)) == 0
 
 
