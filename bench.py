@@ -209,6 +209,17 @@ def main():
     warm_graph.replay()
     ms_warm, _ = timed(warm_graph.replay, a.steps)
 
+    # dispatch floor: a body-less kernel with the same grid, block and LDS size,
+    # K launches replayed as a graph like the convolution (first call eager: it
+    # sets the kernel's LDS attribute, which is not a stream operation)
+    sf.dispatch_floor(B, H, L, plan)
+    floor_graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(floor_graph):
+        for i in range(a.steps):
+            sf.dispatch_floor(B, H, L, plan)
+    floor_graph.replay()
+    ms_floor, _ = timed(floor_graph.replay, a.steps)
+
     # ---- correctness of the measured configuration ----------------------------
     rel_err = None
     if a.check:
@@ -290,6 +301,8 @@ def main():
         "cpu_baseline": cpu,
         "ms_warm": round(ms_warm, 6),
         "ms_eager": round(ms_eager, 6),
+        "ms_dispatch_floor": round(ms_floor, 6),
+        "io_only_frac": round(B * H * L * 2 * s_io / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
         "timing": "HIP graph of the K steps replayed between events; ms_eager: the same steps launched one by one",
         "graph_replay_bitexact": bool(replay_exact),
         "rel_l2_vs_fp64": rel_err,

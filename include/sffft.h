@@ -103,6 +103,12 @@ int sffft_conv_bf16(const uint16_t* u, const void* kf, uint16_t* y, int B, int H
 /* fp32 -> bf16 (round to nearest even) on the device. Replaces tobf16 (src/sffft.cu:306). */
 int sffft_to_bf16(const float* x, uint16_t* y, size_t n, void* stream);
 
+/* Launches a body-less kernel with the grid, block and LDS size that sffft_conv_*
+   uses for this plan and shape: timed back to back, it gives the dispatch floor of
+   that launch shape. No counterpart in the reference (a measurement aid); same
+   argument checks and error codes as sffft_conv_*, without the buffers. */
+int sffft_dispatch_floor(int B, int H, int L, const sffft_plan* plan, void* stream);
+
 /* Copies the device DFT coefficient table (57,344 bytes) to host memory `out`
  * (for tests). Returns SFFFT_EINVAL if out_len is too small. */
 int sffft_dft_table(void* out, size_t out_len);

@@ -102,6 +102,7 @@ def lib() -> ctypes.CDLL:
             "sffft_conv_f32": (ci, [vp, vp, vp, ci, ci, ci, P, vp]),
             "sffft_conv_bf16": (ci, [vp, vp, vp, ci, ci, ci, P, vp]),
             "sffft_to_bf16": (ci, [vp, vp, sz, vp]),
+            "sffft_dispatch_floor": (ci, [ci, ci, ci, P, vp]),
             "sffft_dft_table": (ci, [vp, sz]),
             "sffft_select_candidate": (ci, [ctypes.POINTER(Candidate), ci, ctypes.c_double, ctypes.c_char_p]),
             "sffft_relative_l2": (ctypes.c_double, [ctypes.c_double, ctypes.c_double]),
@@ -231,6 +232,11 @@ def to_bf16(x):
     y = torch.empty(x.shape, dtype=torch.bfloat16, device=x.device)
     _check(lib().sffft_to_bf16(_ptr(x.contiguous()), _ptr(y), x.numel(), _stream()), "sffft_to_bf16")
     return y
+
+
+def dispatch_floor(B: int, H: int, L: int, plan: Plan) -> None:
+    """Launches the body-less kernel with the launch shape of conv() for this plan."""
+    _check(lib().sffft_dispatch_floor(B, H, L, ctypes.byref(plan), _stream()), "sffft_dispatch_floor")
 
 
 def dft_table():

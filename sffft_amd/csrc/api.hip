@@ -322,6 +322,11 @@ float last_stage_scale(const sffft_plan* p) {
 
 bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
+// Body-less kernel: launched with a plan's grid, block and LDS size it measures the
+// dispatch cost of that launch shape (workgroup dispatch, LDS allocation, wave
+// launch and retirement) without any memory traffic.
+__global__ void empty_dispatch_kernel() {}
+
 template <int IO>
 int conv(const void* u, const void* kf, void* y, int B, int H, int L, const sffft_plan* p, void* stream) {
   if (!u || !kf || !y || B < 1 || H < 1 || (long long)B * H > INT_MAX) return SFFFT_EINVAL;
@@ -447,6 +452,28 @@ int sffft_conv_f32(const float* u, const void* kf, float* y, int B, int H, int L
 int sffft_conv_bf16(const uint16_t* u, const void* kf, uint16_t* y, int B, int H, int L, const sffft_plan* plan,
                     void* stream) {
   return conv<1>(u, kf, y, B, H, L, plan, stream);
+}
+
+int sffft_dispatch_floor(int B, int H, int L, const sffft_plan* plan, void* stream) {
+  if (B < 1 || H < 1 || (long long)B * H > INT_MAX) return SFFFT_EINVAL;
+  int rc = check_shape(L, plan);
+  if (rc) return rc;
+  if (B % plan->seqs) return SFFFT_EINVAL;
+  const Entry* e = find_entry(L, plan);
+  if (!e) return SFFFT_ENOPLAN;
+  const unsigned grid = e->mode == 1 ? (unsigned)((H + e->channels - 1) / e->channels)
+                                     : (unsigned)(H * (B / plan->seqs));
+  static std::once_flag attr_once;
+  static int attr_rc = SFFFT_OK;
+  std::call_once(attr_once, [] {
+    attr_rc = hip_status(hipFuncSetAttribute(reinterpret_cast<const void*>(&empty_dispatch_kernel),
+                                             hipFuncAttributeMaxDynamicSharedMemorySize, 163840),
+                         "hipFuncSetAttribute");
+  });
+  if (attr_rc) return attr_rc;
+  hipLaunchKernelGGL(empty_dispatch_kernel, dim3(grid), dim3(64 * plan->waves), (unsigned)e->lds_bytes,
+                     (hipStream_t)stream);
+  return hip_status(hipGetLastError(), "dispatch floor launch");
 }
 
 int sffft_to_bf16(const float* x, uint16_t* y, size_t n, void* stream) {

@@ -67,6 +67,10 @@ def test_conv_argument_errors_need_no_gpu():
     assert lib.sffft_conv_bf16(good, good, good, 0, 768, 1024, ctypes.byref(p), null) == sf.SFFFT_EINVAL
     assert lib.sffft_spectrum(good, 768, 1024, ctypes.byref(p), good, good, null) == sf.SFFFT_EINVAL  # kf == work
     assert sf.lib().sffft_spectrum_bytes(768, 1024) == 768 * 2048 * 8
+    # the dispatch floor checks its shape like conv, before any HIP call
+    assert lib.sffft_dispatch_floor(0, 768, 1024, ctypes.byref(p), null) == sf.SFFFT_EINVAL
+    assert lib.sffft_dispatch_floor(7, 768, 1024, ctypes.byref(p), null) == sf.SFFFT_EINVAL  # B odd
+    assert lib.sffft_dispatch_floor(8, 768, 1000, ctypes.byref(p), null) == sf.SFFFT_EINVAL  # L
 
 
 def test_strerror():
