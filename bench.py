@@ -30,7 +30,7 @@ DEFAULT_PLANS = {  # (plan, waves, seqs, mode, channels per workgroup) per (L, i
     (256, "fp32"): ("32x16", 12, 2, 1, 3), (256, "bf16"): ("32x16", 12, 2, 1, 3),
     (512, "fp32"): ("32x32", 12, 2, 1, 3), (512, "bf16"): ("32x32", 12, 2, 1, 3),
     (1024, "fp32"): ("64x32", 12, 2, 1, 3), (1024, "bf16"): ("64x32", 12, 2, 1, 3),
-    (2048, "fp32"): ("64x64", 4, 2, 1, 1), (2048, "bf16"): ("64x64", 4, 2, 1, 1),
+    (2048, "fp32"): ("64x64", 12, 2, 1, 3), (2048, "bf16"): ("64x64", 12, 2, 1, 3),
     (4096, "fp32"): ("32x16x16", 8, 2, 0, 1), (4096, "bf16"): ("32x16x16", 8, 2, 0, 1),
     (8192, "fp32"): ("32x32x16", 4, 2, 0, 1), (8192, "bf16"): ("64x16x16", 8, 2, 0, 1),
     (16384, "fp32"): ("32x32x32", 8, 1, 0, 1), (16384, "bf16"): ("32x32x32", 8, 2, 0, 1),

@@ -38,10 +38,15 @@ bool valid_waves(int w, int mode) {
 // not compiled.
 size_t lds_bytes_rt(int r0, int r1, int r2, int mode, int channels, int waves) {
   if (mode == 1) {
-    const int T0 = r0 / 16, T1 = r1 / 16;
-    // DFT fragments, two twiddle tables, the channel spectra, the per-wave operand scratch
-    return (size_t)(T0 * T0 * 128 + (r1 == r0 ? 0 : T1 * T1 * 128) + r0 * r1 + channels * r0 * r1 / 2) * 16 +
-           (size_t)waves * 16 * (r1 + 4) * 4;
+    // WavePlan::lds_bytes: DFT fragments and the twiddle tables (one when r0 == r1);
+    // then, in order of preference, row-load scratch and spectra, spectra alone
+    // (strided loads), or the scratch alone (spectra read from global memory)
+    const int T0 = r0 / 16, T1 = r1 / 16, N = r0 * r1;
+    const size_t tab = (size_t)(T0 * T0 * 128 + (r1 == r0 ? 0 : T1 * T1 * 128) + (r1 == r0 ? 1 : 2) * N / 2) * 16;
+    const size_t scratch = (size_t)waves * 16 * (r1 + 4) * 4, spectra = (size_t)channels * N / 2 * 16;
+    const bool rows = tab + spectra + scratch <= 163840 || tab + spectra > 163840;
+    const bool in_lds = tab + spectra + (rows ? scratch : 0) <= 163840;
+    return tab + (in_lds ? spectra : 0) + (rows ? scratch : 0);
   }
   const int S = r2 > 1 ? 3 : 2, N = r0 * r1 * r2, M = N / r0;
   const int PA = r1 + LDS_PAD, PB = r0 + LDS_PAD, PC = r2 + LDS_PAD;
@@ -157,6 +162,8 @@ int device_table(const void** out) {
 // TW1[tile mt*ST+nt][lane (c,g)][v] = sc0 * w^(m k0),        m = 16mt+4g+v, k0 = 16nt+c
 // TW2[tile s*MT+t][lane (c,g)][v]   = sc0 * sc1 * w^(k0 n1), k0 = 16s+4g+v,  n1 = 16t+c
 // with w = exp(-2 pi i / N), sc = 1/sqrt(R); exponents reduced mod N, fp64 then fp32.
+// Square plans (r0 == r1) read TW1 only: TW2 equals it index for index up to sc1,
+// which their spectrum carries instead (last_stage_scale).
 void build_twiddles(int r0, int r1, std::vector<float>& t) {
   const int N = r0 * r1, ST = r0 / 16, MT = r1 / 16;
   const double two_pi = 6.283185307179586476925286766559;
@@ -315,8 +322,11 @@ __global__ void to_bf16_kernel(const float* __restrict__ x, uint16_t* __restrict
   if (i < n) y[i] = f32_to_bf16(x[i]);
 }
 
+// Scale folded into the kernel-order spectrum: 1/sqrt(R) of the last radix; square
+// wave plans also carry the 1/sqrt(R1) of their shared twiddle table (1/R1 in all).
 float last_stage_scale(const sffft_plan* p) {
   const int R = p->r2 > 1 ? p->r2 : p->r1;
+  if (p->mode == 1 && p->r0 == p->r1) return (float)(1.0 / (double)R);
   return (float)(1.0 / std::sqrt((double)R));
 }
 

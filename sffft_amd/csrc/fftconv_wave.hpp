@@ -28,7 +28,12 @@
 //   TW1    : sc0 * w^(m k0) in the lane order of the phase-1 result tiles
 //   TW2    : sc1 * sc0 * w^(k0 n1) in the lane order of the inverse result tiles
 // so no twiddle is evaluated in the loop and no per-stage scale is applied; the
-// output scale 1/sqrt(R0) rides on TW2 and 1/sqrt(R1) on the spectrum.
+// output scale 1/sqrt(R0) rides on TW2 and 1/sqrt(R1) on the spectrum. With
+// R0 == R1 the two tables hold the same function of the same tile and lane
+// indices, so TW2 is TW1 and the spectrum carries sc1 as well (1/R1).
+// The channel spectra sit in LDS when they fit beside the tables and the operand
+// scratch; otherwise the wavefronts read them from global memory (L2-resident:
+// B/2 wavefronts read each channel's spectrum).
 #pragma once
 #include "fftconv.hpp"
 
@@ -45,10 +50,23 @@ struct WavePlan {
   static constexpr int F1_H8 = R1 == R0 ? 0 : MT * MT * 128;
   static constexpr int TW_F4 = N / 2;  // one twiddle table: N complex fp32 = N/2 float4
   static constexpr int SP_F4 = N / 2;  // one channel's spectrum: N complex64 = N/2 float4
-  static constexpr int TAB_F4 = F0_H8 + F1_H8 + 2 * TW_F4;
-  // LDS of a workgroup of nw wavefronts holding `ch` channel spectra, with the
-  // per-wavefront operand scratch of fp32 I/O (bf16 needs less)
-  static constexpr int lds_bytes(int ch, int nw) { return (TAB_F4 + ch * SP_F4) * 16 + nw * 16 * (M + 4) * 4; }
+  static constexpr int TW_TABLES = R0 == R1 ? 1 : 2;
+  static constexpr int TAB_F4 = F0_H8 + F1_H8 + TW_TABLES * TW_F4;
+  // per-wavefront operand scratch of the row loads with fp32 I/O (bf16 needs less)
+  static constexpr int SCRATCH_MAX = 16 * (M + 4) * 4;
+  // Layout choice for a workgroup of nw wavefronts serving ch channels, in order of
+  // preference: row loads and spectra in LDS; strided loads (no scratch) and spectra
+  // in LDS; row loads and spectra read from global memory.
+  static constexpr int tables_and_spectra_bytes(int ch) { return (TAB_F4 + ch * SP_F4) * 16; }
+  static constexpr bool row_loads(int ch, int nw) {
+    return tables_and_spectra_bytes(ch) + nw * SCRATCH_MAX <= 163840 || tables_and_spectra_bytes(ch) > 163840;
+  }
+  static constexpr bool spectra_in_lds(int ch, int nw) {
+    return tables_and_spectra_bytes(ch) + (row_loads(ch, nw) ? nw * SCRATCH_MAX : 0) <= 163840;
+  }
+  static constexpr int lds_bytes(int ch, int nw) {
+    return (TAB_F4 + (spectra_in_lds(ch, nw) ? ch * SP_F4 : 0)) * 16 + (row_loads(ch, nw) ? nw * SCRATCH_MAX : 0);
+  }
   static_assert(R0 >= 16 && R0 <= 64 && R1 >= 16 && R1 <= 64, "radices are 16, 32 or 64");
 };
 
@@ -164,22 +182,54 @@ __device__ __forceinline__ void compute_dft(h8* dst, int tid) {
 // the pair (rows a then b) goes to lane q % 64 of round q / 64.
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
+template <class P, class TIO, bool ROWS>
+struct PairLoads;
+
 template <class P, class TIO>
-struct PairLoads {
+struct PairLoads<P, TIO, true> {
   static constexpr int EPC = 16 / (int)sizeof(TIO);  // samples per chunk
   static constexpr int CPS = P::L / EPC;              // chunks per row
   static constexpr int ROUNDS = (2 * CPS + 63) / 64;  // load instructions per pair
+  static constexpr int ISSUES = ROUNDS;
   u32x4 c[ROUNDS];
 };
 
-// Vector-memory instructions issue_pair_loads emits.
+// Strided loads (no LDS scratch): lane (r, g) loads its own operand elements,
+// n0 = 16ks + 4g + j, m = 16mt + r, one instruction per element (64-byte runs).
 template <class P, class TIO>
-__host__ __device__ constexpr int pair_load_issues() { return PairLoads<P, TIO>::ROUNDS; }
+struct PairLoads<P, TIO, false> {
+  static constexpr int ISSUES = P::MT * P::KS1 * 8;
+  TIO raw[P::MT][P::KS1][8];
+};
+
+// Vector-memory instructions issue_pair_loads emits.
+template <class P, class TIO, bool ROWS>
+__host__ __device__ constexpr int pair_load_issues() { return PairLoads<P, TIO, ROWS>::ISSUES; }
 
 template <class P, class TIO>
 __device__ __forceinline__ void issue_pair_loads(const TIO* __restrict__ xa, const TIO* __restrict__ xb,
-                                                 PairLoads<P, TIO>& d, int lane) {
-  typedef PairLoads<P, TIO> D;
+                                                 PairLoads<P, TIO, false>& d, int lane) {
+  constexpr int R0 = P::R0, M = P::M, MT = P::MT;
+  const int r = lane & 15, g = lane >> 4;
+  // lane bases at (n0 = 4g, m = r); every element is a constant offset from them
+  const TIO* pa = xa + (4 * g * M + r);
+  const TIO* pb = xb + (4 * g * M + r);
+  const bool live = R0 >= 32 || 4 * g < R0 / 2;  // R0 = 16: rows n0 >= 8 are the zero padding
+#pragma unroll
+  for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+    for (int ks = 0; ks < P::KS1; ks++)
+#pragma unroll
+      for (int j = 0; j < 8; j++) {
+        const int off = (16 * ks + (j & 3)) * M + 16 * mt;
+        d.raw[mt][ks][j] = live ? (j < 4 ? pa[off] : pb[off]) : (TIO)0;
+      }
+}
+
+template <class P, class TIO>
+__device__ __forceinline__ void issue_pair_loads(const TIO* __restrict__ xa, const TIO* __restrict__ xb,
+                                                 PairLoads<P, TIO, true>& d, int lane) {
+  typedef PairLoads<P, TIO, true> D;
 #pragma unroll
   for (int i = 0; i < D::ROUNDS; i++) {
     const int q = i * 64 + lane;
@@ -204,9 +254,34 @@ __device__ __forceinline__ float io_to_f32_lds(const uint16_t* p) { return __uin
 
 // Phase-1 A operands a[mt][ks] (slots 0..3 row a, 4..7 row b; n0 = 16ks + 4g + j,
 // m = 16mt + r) from the pair's chunks, through the wave's scratch S.
+// 0 that the compiler cannot see through: added to the raw bits of the first pair's
+// strided operands, it keeps their conversion below the workgroup barrier (hoisted
+// above it, the conversion would make the wave wait for its loads there).
+__device__ __forceinline__ uint32_t opaque_zero() {
+  uint32_t v;
+  __asm__ volatile("v_mov_b32 %0, 0" : "=v"(v));
+  return v;
+}
+__device__ __forceinline__ float io_bits_to_f32(float x, uint32_t z) { return __uint_as_float(__float_as_uint(x) + z); }
+__device__ __forceinline__ float io_bits_to_f32(uint16_t x, uint32_t z) {
+  return __uint_as_float(((uint32_t)x + z) << 16);
+}
+
 template <class P, class TIO>
-__device__ __forceinline__ void pair_operands(const PairLoads<P, TIO>& d, TIO* S, h8 (*a)[P::KS1], int lane) {
-  typedef PairLoads<P, TIO> D;
+__device__ __forceinline__ void pair_operands(const PairLoads<P, TIO, false>& d, TIO*, uint32_t z, h8 (*a)[P::KS1],
+                                              int) {
+#pragma unroll
+  for (int mt = 0; mt < P::MT; mt++)
+#pragma unroll
+    for (int ks = 0; ks < P::KS1; ks++)
+#pragma unroll
+      for (int j = 0; j < 8; j++) a[mt][ks][j] = (_Float16)io_bits_to_f32(d.raw[mt][ks][j], z);
+}
+
+template <class P, class TIO>
+__device__ __forceinline__ void pair_operands(const PairLoads<P, TIO, true>& d, TIO* S, uint32_t, h8 (*a)[P::KS1],
+                                              int lane) {
+  typedef PairLoads<P, TIO, true> D;
   constexpr int R0 = P::R0, M = P::M, PITCH = scratch_pitch<P, TIO>();
   constexpr int ROWS = R0 / 2 < 16 ? R0 / 2 : 16;  // non-zero rows per K step
   const int r = lane & 15, g = lane >> 4;
@@ -245,19 +320,27 @@ __device__ __forceinline__ void pair_operands(const PairLoads<P, TIO>& d, TIO* S
 
 // Every stage of one pair, from its loaded operands to the stored outputs; SP is the
 // channel's spectrum in LDS.
-template <class P, class TIO, bool ACC16, bool HOLD_F1>
-__device__ __forceinline__ void process_pair(const PairLoads<P, TIO>& d, TIO* S, const float4* SP,
+template <class P, class TIO, bool ACC16, bool HOLD_F1, bool ROWS>
+__device__ __forceinline__ void process_pair(const PairLoads<P, TIO, ROWS>& d, TIO* S, uint32_t z, const float4* SP,
                                              TIO* __restrict__ ya, TIO* __restrict__ yb, const h8* F0,
                                              const h8* F1, const float4* TW1, const float4* TW2, int lane) {
   constexpr int R0 = P::R0, M = P::M, MT = P::MT, ST = P::ST, KS1 = P::KS1, NT3 = P::NT3;
   const int r = lane & 15, g = lane >> 4;
+  // With 16 tiles per transform (64x64) the pair alone fills 64 VGPRs; compiler-only
+  // barriers at the top of each tile step keep the next step's table and spectrum
+  // loads from being hoisted over the current one, which would not fit beside it.
+  constexpr bool LEAN = MT * ST >= 16;
+  auto step_fence = [] {
+    if constexpr (LEAN) __asm__ volatile("" ::: "memory");
+  };
 
   // ---- phase 1: DFT over n0 (first R0/2 rows only), twiddle, -> B2[m tile][k0 strip]
   h8 a[MT][KS1];
-  pair_operands<P, TIO>(d, S, a, lane);
+  pair_operands<P, TIO>(d, S, z, a, lane);
   h8 b2[MT][ST];
 #pragma unroll
   for (int nt = 0; nt < ST; nt++) {
+    step_fence();
     h8 f0[KS1], f1[KS1];
 #pragma unroll
     for (int ks = 0; ks < KS1; ks++) {
@@ -298,6 +381,7 @@ __device__ __forceinline__ void process_pair(const PairLoads<P, TIO>& d, TIO* S,
     h8 a2[MT];
 #pragma unroll
     for (int kt = 0; kt < MT; kt++) {
+      step_fence();
       f4 dr = {0.f, 0.f, 0.f, 0.f}, di = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int mt = 0; mt < MT; mt++) {
@@ -311,6 +395,7 @@ __device__ __forceinline__ void process_pair(const PairLoads<P, TIO>& d, TIO* S,
     }
 #pragma unroll
     for (int t = 0; t < MT; t++) {
+      step_fence();
       f4 er = {0.f, 0.f, 0.f, 0.f}, ei = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int kt = 0; kt < MT; kt++) {
@@ -327,6 +412,7 @@ __device__ __forceinline__ void process_pair(const PairLoads<P, TIO>& d, TIO* S,
   // ---- phase 3: inverse DFT over k0 for n0 < R0/2; real part -> row a, -imag -> row b
 #pragma unroll
   for (int nu = 0; nu < NT3; nu++) {
+    step_fence();
     h8 f0[ST], f1[ST];
 #pragma unroll
     for (int s = 0; s < ST; s++) {
@@ -368,21 +454,24 @@ __global__ void __launch_bounds__(64 * NW)
     fftconv_wave_kernel(const TIO* __restrict__ u, const float4* __restrict__ kf, TIO* __restrict__ y, int B,
                         int H, const h8* __restrict__ ftab, const float4* __restrict__ twtab) {
   constexpr int R0 = P::R0;
-  constexpr int SCR_F4 = scratch_bytes<P, TIO>() / 16;
-  __shared__ float4 lds[P::TAB_F4 + CH * P::SP_F4 + NW * SCR_F4];
+  constexpr bool ROWS = P::row_loads(CH, NW);
+  constexpr int SCR_F4 = ROWS ? scratch_bytes<P, TIO>() / 16 : 0;
+  constexpr bool SP_LDS = P::spectra_in_lds(CH, NW);
+  constexpr int SPL_F4 = SP_LDS ? CH * P::SP_F4 : 0;
+  __shared__ float4 lds[P::TAB_F4 + SPL_F4 + NW * SCR_F4];
   h8* F0 = reinterpret_cast<h8*>(lds);
   h8* F1 = P::R1 == P::R0 ? F0 : F0 + P::F0_H8;
   float4* TW1 = lds + P::F0_H8 + P::F1_H8;
-  float4* TW2 = TW1 + P::TW_F4;
+  float4* TW2 = P::TW_TABLES == 2 ? TW1 + P::TW_F4 : TW1;
   float4* SPL = lds + P::TAB_F4;
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  TIO* S = reinterpret_cast<TIO*>(lds + P::TAB_F4 + CH * P::SP_F4 + wave * SCR_F4);
+  TIO* S = reinterpret_cast<TIO*>(lds + P::TAB_F4 + SPL_F4 + wave * SCR_F4);
   const int BP = B >> 1, h0 = blockIdx.x * CH;
   const int nch = H - h0 < CH ? H - h0 : CH;  // channels of this workgroup
 
   // ---- tables and spectra: direct global -> LDS copies, issued first
-  dma_to_lds<2 * P::TW_F4, NW>(TW1, [&](int k) { return twtab + k; }, lane, wave);
+  dma_to_lds<P::TW_TABLES * P::TW_F4, NW>(TW1, [&](int k) { return twtab + k; }, lane, wave);
   if constexpr (CACHED) {
     dma_to_lds<P::F0_H8, NW>(reinterpret_cast<float4*>(F0), [&](int k) {
       return reinterpret_cast<const float4*>(ftab + cf_off(R0) + k);
@@ -392,13 +481,18 @@ __global__ void __launch_bounds__(64 * NW)
         return reinterpret_cast<const float4*>(ftab + cf_off(P::R1) + k);
       }, lane, wave);
   }
-  {
+  if constexpr (SP_LDS) {
     // channel c of this workgroup is in slot c; slots past the last channel copy
     // the last channel again (in bounds, never read)
     const float4* src = kf + (size_t)h0 * P::SP_F4;
     const int last = nch * P::SP_F4 - 1;
     dma_to_lds<CH * P::SP_F4, NW>(SPL, [&](int k) { return src + (k < last ? k : last); }, lane, wave);
   }
+  // spectrum of channel slot c: in LDS, or the channel's row in global memory
+  auto spec = [&](int c) -> const float4* {
+    if constexpr (SP_LDS) return SPL + c * P::SP_F4;
+    else return kf + (size_t)(h0 + c) * P::SP_F4;
+  };
   if constexpr (!CACHED) {
     compute_dft<R0, 64 * NW>(F0, tid);
     if constexpr (P::R1 != P::R0) compute_dft<P::R1, 64 * NW>(F1, tid);
@@ -412,7 +506,7 @@ __global__ void __launch_bounds__(64 * NW)
   // after the barrier, so the first channel's data lands (and is computed and
   // stored) while the rest is still in flight.
   const int npairs = nch * BP;
-  PairLoads<P, TIO> cur;
+  PairLoads<P, TIO, ROWS> cur;
   auto issue_first = [&]() {
     const int c = wave / BP, bp = wave - c * BP;
     const size_t ra = ((size_t)(2 * bp) * H + h0 + c) * P::L;
@@ -422,7 +516,7 @@ __global__ void __launch_bounds__(64 * NW)
   __asm__ volatile("" ::: "memory");
   if (early) {
     issue_first();
-    wait_vmcnt<pair_load_issues<P, TIO>()>();
+    wait_vmcnt<pair_load_issues<P, TIO, ROWS>()>();
   } else {
     wait_vmcnt<0>();
   }
@@ -438,17 +532,22 @@ __global__ void __launch_bounds__(64 * NW)
   if (wave < npairs) {
     const int c = wave / BP, bp = wave - c * BP;
     const size_t ra = ((size_t)(2 * bp) * H + h0 + c) * P::L, rb = ra + (size_t)H * P::L;
-    process_pair<P, TIO, ACC16, HOLD>(cur, S, SPL + c * P::SP_F4, y + ra, y + rb, F0, F1, TW1, TW2,
+    process_pair<P, TIO, ACC16, HOLD>(cur, S, ROWS ? 0u : opaque_zero(), spec(c), y + ra, y + rb, F0, F1, TW1, TW2,
                                       lane);
   }
   for (int p = wave + NW; p < npairs; p += NW) {
     // compiler-only barrier: keeps the table reads inside the loop (hoisting them
     // would pin every twiddle tile in VGPRs)
     __asm__ volatile("" ::: "memory");
+    // 64x64: the lane index is made opaque per iteration, so the per-lane addresses
+    // derived from it are recomputed here instead of being hoisted out of the loop
+    // and kept live (spilled) across it
+    int ln = lane;
+    if constexpr (P::MT * P::ST >= 16) __asm__ volatile("" : "+v"(ln));
     const int c = p / BP, bp = p - c * BP;
     const size_t ra = ((size_t)(2 * bp) * H + h0 + c) * P::L, rb = ra + (size_t)H * P::L;
-    issue_pair_loads<P, TIO>(u + ra, u + rb, cur, lane);
-    process_pair<P, TIO, ACC16, HOLD>(cur, S, SPL + c * P::SP_F4, y + ra, y + rb, F0, F1, TW1, TW2, lane);
+    issue_pair_loads<P, TIO>(u + ra, u + rb, cur, ln);
+    process_pair<P, TIO, ACC16, HOLD>(cur, S, 0u, spec(c), y + ra, y + rb, F0, F1, TW1, TW2, ln);
   }
 }
 
