@@ -318,6 +318,40 @@ __device__ __forceinline__ void pair_operands(const PairLoads<P, TIO, true>& d, 
     }
 }
 
+// Output of one 16-row block (rows n0 = 16nu + c of the MT result tiles; lane (c, g)
+// holds m = 16t + 4g .. +3 of tile t) of one sequence, through the wave's scratch S,
+// so that every store instruction writes whole rows: lane q of round i stores
+// 16-byte chunk q % CPR of row q / CPR (for fp32 rows of 32 samples, 8 rows of 128
+// bytes, one KB contiguous). Streaming stores of partial lines would reach HBM as
+// partial writes. Rows from ROWS3 on (the zero half of R0 = 16) are not stored.
+__device__ __forceinline__ void put4(float* p, f4 v) { *reinterpret_cast<f4*>(p) = v; }
+__device__ __forceinline__ void put4(uint16_t* p, f4 v) {
+  typedef float fl2 __attribute__((ext_vector_type(2)));
+  typedef __bf16 bf2 __attribute__((ext_vector_type(2)));
+  const bf2 lo = __builtin_convertvector((fl2){v[0], v[1]}, bf2);  // round to nearest even
+  const bf2 hi = __builtin_convertvector((fl2){v[2], v[3]}, bf2);
+  *reinterpret_cast<u32x2*>(p) = (u32x2){__builtin_bit_cast(uint32_t, lo), __builtin_bit_cast(uint32_t, hi)};
+}
+
+template <class P, class TIO>
+__device__ __forceinline__ void store_rows(TIO* S, const f4 (&z)[P::MT], TIO* __restrict__ y, int lane) {
+  constexpr int M = P::M, PITCH = scratch_pitch<P, TIO>(), EPC = 16 / (int)sizeof(TIO), CPR = M / EPC;
+  constexpr int ROWS3 = P::R0 >= 32 ? 16 : P::R0 / 2, ROUNDS = (16 * CPR + 63) / 64;
+  const int c = lane & 15, g = lane >> 4;
+#pragma unroll
+  for (int t = 0; t < P::MT; t++) put4(S + c * PITCH + 16 * t + 4 * g, z[t]);
+  // other lanes' writes are read below (see pair_operands)
+  __asm__ volatile("" ::: "memory");
+#pragma unroll
+  for (int i = 0; i < ROUNDS; i++) {
+    const int q = i * 64 + lane, row = q / CPR, col = (q % CPR) * EPC;
+    if (row < ROWS3)
+      __builtin_nontemporal_store(*reinterpret_cast<const u32x4*>(S + row * PITCH + col),
+                                  reinterpret_cast<u32x4*>(y + row * M + col));
+  }
+  __asm__ volatile("" ::: "memory");
+}
+
 // Every stage of one pair, from its loaded operands to the stored outputs; SP is the
 // channel's spectrum in LDS.
 template <class P, class TIO, bool ACC16, bool HOLD_F1, bool ROWS>
@@ -420,26 +454,33 @@ __device__ __forceinline__ void process_pair(const PairLoads<P, TIO, ROWS>& d, T
       f1[s] = dft_frag<R0>(F0, nu, s, 1, lane);
     }
     const int n0 = 16 * nu + r;
+    f4 za[MT] = {}, zb[MT] = {};
 #pragma unroll
     for (int t = 0; t < MT; t++) {
-      f4 za = {0.f, 0.f, 0.f, 0.f}, zb = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int s = 0; s < ST; s++) {
-        za = mfma(b2[t][s], f0[s], za);
-        zb = mfma(b2[t][s], f1[s], zb);
+        za[t] = mfma(b2[t][s], f0[s], za[t]);
+        zb[t] = mfma(b2[t][s], f1[s], zb[t]);
       }
-      za = acc_round<ACC16>(za);
-      zb = -acc_round<ACC16>(zb);  // row b is minus the imaginary part
-      if (R0 >= 32 || n0 < R0 / 2) {
-        const int o = n0 * M + 16 * t + 4 * g;
-        store4(ya + o, za);
-        store4(yb + o, zb);
+      za[t] = acc_round<ACC16>(za[t]);
+      zb[t] = -acc_round<ACC16>(zb[t]);  // row b is minus the imaginary part
+      if constexpr (!ROWS) {
+        // no scratch: each lane stores its own 16-byte (fp32) or 8-byte (bf16) piece
+        if (R0 >= 32 || n0 < R0 / 2) {
+          const int o = n0 * M + 16 * t + 4 * g;
+          store4(ya + o, za[t]);
+          store4(yb + o, zb[t]);
+        }
+        // With one tile per axis (MT == 1) the loop runs once and the store
+        // addresses are loop-invariant: loop store promotion would re-create the
+        // stores without their non-temporal hint. A compiler-only barrier prevents
+        // that (with MT > 1 it would only constrain scheduling).
+        if constexpr (MT == 1) __asm__ volatile("" ::: "memory");
       }
-      // With one tile per axis (MT == 1) the loop runs once and the store addresses
-      // are loop-invariant: loop store promotion would re-create the stores without
-      // their non-temporal hint. A compiler-only barrier prevents that (with MT > 1
-      // it would only constrain scheduling).
-      if constexpr (MT == 1) __asm__ volatile("" ::: "memory");
+    }
+    if constexpr (ROWS) {
+      store_rows<P, TIO>(S, za, ya + 16 * nu * M, lane);
+      store_rows<P, TIO>(S, zb, yb + 16 * nu * M, lane);
     }
   }
 }
@@ -539,11 +580,11 @@ __global__ void __launch_bounds__(64 * NW)
     // compiler-only barrier: keeps the table reads inside the loop (hoisting them
     // would pin every twiddle tile in VGPRs)
     __asm__ volatile("" ::: "memory");
-    // 64x64: the lane index is made opaque per iteration, so the per-lane addresses
-    // derived from it are recomputed here instead of being hoisted out of the loop
-    // and kept live (spilled) across it
+    // the lane index is made opaque per iteration, so the per-lane addresses derived
+    // from it are recomputed here instead of being hoisted out of the loop and kept
+    // live (or spilled) across it
     int ln = lane;
-    if constexpr (P::MT * P::ST >= 16) __asm__ volatile("" : "+v"(ln));
+    __asm__ volatile("" : "+v"(ln));
     const int c = p / BP, bp = p - c * BP;
     const size_t ra = ((size_t)(2 * bp) * H + h0 + c) * P::L, rb = ra + (size_t)H * P::L;
     issue_pair_loads<P, TIO>(u + ra, u + rb, cur, ln);
