@@ -92,14 +92,7 @@ __device__ __forceinline__ uint16_t f32_to_bf16(float f) {
   return (uint16_t)(x >> 16);
 }
 
-// Output stores carry the streaming (non-temporal) hint. Each output line is written
-// once and never read by the kernel; held dirty in the XCD's L2 it would be written
-// back by the end-of-kernel release, after the last wave, instead of during the run.
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
-__device__ __forceinline__ void stream_store(float* p, f4 v) { __builtin_nontemporal_store(v, reinterpret_cast<f4*>(p)); }
-__device__ __forceinline__ void stream_store(uint16_t* p, uint32_t lo, uint32_t hi) {
-  __builtin_nontemporal_store((u32x2){lo, hi}, reinterpret_cast<u32x2*>(p));
-}
 // fp16-accumulation mode: the raw tile accumulator is rounded to fp16 (range and
 // rounding of an fp16 accumulator; +-inf beyond 65504).
 __device__ __forceinline__ f4 round_acc(f4 v, int acc16) {
@@ -586,19 +579,21 @@ __device__ __forceinline__ void phase3(TIO* __restrict__ ya, TIO* __restrict__ y
     const int n0 = 16 * nt + r;
     if (n0 < R0 / 2) {
       const int o = n0 * M + 16 * mt + 4 * g;
+      // Plain (write-back) stores: the 64- or 32-byte pieces of one output line come
+      // from different wavefronts, and L2 merges them before they reach HBM
+      // (streaming stores would write each piece separately).
       if constexpr (sizeof(TIO) == 4) {
-        stream_store(ya + o, zr * sc0);
-        if constexpr (NSEQ == 2) stream_store(yb + o, zi * -sc0);
+        *reinterpret_cast<f4*>(ya + o) = zr * sc0;
+        if constexpr (NSEQ == 2) *reinterpret_cast<f4*>(yb + o) = zi * -sc0;
       } else {
-        stream_store(ya + o, (uint32_t)f32_to_bf16(zr[0] * sc0) | ((uint32_t)f32_to_bf16(zr[1] * sc0) << 16),
-                     (uint32_t)f32_to_bf16(zr[2] * sc0) | ((uint32_t)f32_to_bf16(zr[3] * sc0) << 16));
+        *reinterpret_cast<u32x2*>(ya + o) =
+            (u32x2){(uint32_t)f32_to_bf16(zr[0] * sc0) | ((uint32_t)f32_to_bf16(zr[1] * sc0) << 16),
+                    (uint32_t)f32_to_bf16(zr[2] * sc0) | ((uint32_t)f32_to_bf16(zr[3] * sc0) << 16)};
         if constexpr (NSEQ == 2)
-          stream_store(yb + o, (uint32_t)f32_to_bf16(-zi[0] * sc0) | ((uint32_t)f32_to_bf16(-zi[1] * sc0) << 16),
-                       (uint32_t)f32_to_bf16(-zi[2] * sc0) | ((uint32_t)f32_to_bf16(-zi[3] * sc0) << 16));
+          *reinterpret_cast<u32x2*>(yb + o) =
+              (u32x2){(uint32_t)f32_to_bf16(-zi[0] * sc0) | ((uint32_t)f32_to_bf16(-zi[1] * sc0) << 16),
+                      (uint32_t)f32_to_bf16(-zi[2] * sc0) | ((uint32_t)f32_to_bf16(-zi[3] * sc0) << 16)};
       }
-      // compiler-only barrier: loop store promotion would re-create the stores
-      // without their non-temporal hint
-      __asm__ volatile("" ::: "memory");
     }
   };
   auto load = [&](int mt, h8* a) {

@@ -119,13 +119,15 @@ __device__ __forceinline__ f4 acc_round(f4 v) {
 
 __device__ __forceinline__ float4 ld_f4(const float4* p) { return *p; }
 
-__device__ __forceinline__ void store4(float* p, f4 v) { stream_store(p, v); }
+// Per-lane output pieces (plans without the operand scratch): plain write-back
+// stores, so L2 merges the partial lines before they reach HBM.
+__device__ __forceinline__ void store4(float* p, f4 v) { *reinterpret_cast<f4*>(p) = v; }
 __device__ __forceinline__ void store4(uint16_t* p, f4 v) {
   typedef float fl2 __attribute__((ext_vector_type(2)));
   typedef __bf16 bf2 __attribute__((ext_vector_type(2)));
   const bf2 lo = __builtin_convertvector((fl2){v[0], v[1]}, bf2);  // round to nearest even
   const bf2 hi = __builtin_convertvector((fl2){v[2], v[3]}, bf2);
-  stream_store(p, __builtin_bit_cast(uint32_t, lo), __builtin_bit_cast(uint32_t, hi));
+  *reinterpret_cast<u32x2*>(p) = (u32x2){__builtin_bit_cast(uint32_t, lo), __builtin_bit_cast(uint32_t, hi)};
 }
 
 // 16-byte blocks copied from global memory straight into LDS (global_load_lds_dwordx4:
@@ -322,8 +324,11 @@ __device__ __forceinline__ void pair_operands(const PairLoads<P, TIO, true>& d, 
 // holds m = 16t + 4g .. +3 of tile t) of one sequence, through the wave's scratch S,
 // so that every store instruction writes whole rows: lane q of round i stores
 // 16-byte chunk q % CPR of row q / CPR (for fp32 rows of 32 samples, 8 rows of 128
-// bytes, one KB contiguous). Streaming stores of partial lines would reach HBM as
-// partial writes. Rows from ROWS3 on (the zero half of R0 = 16) are not stored.
+// bytes, one KB contiguous). Whole lines allow the streaming (non-temporal) hint:
+// each line is written once, and held dirty in the XCD's L2 it would be written back
+// by the end-of-kernel release after the last wave instead of during the run
+// (streaming stores of partial lines would reach HBM as partial writes).
+// Rows from ROWS3 on (the zero half of R0 = 16) are not stored.
 __device__ __forceinline__ void put4(float* p, f4 v) { *reinterpret_cast<f4*>(p) = v; }
 __device__ __forceinline__ void put4(uint16_t* p, f4 v) {
   typedef float fl2 __attribute__((ext_vector_type(2)));
@@ -471,11 +476,6 @@ __device__ __forceinline__ void process_pair(const PairLoads<P, TIO, ROWS>& d, T
           store4(ya + o, za[t]);
           store4(yb + o, zb[t]);
         }
-        // With one tile per axis (MT == 1) the loop runs once and the store
-        // addresses are loop-invariant: loop store promotion would re-create the
-        // stores without their non-temporal hint. A compiler-only barrier prevents
-        // that (with MT > 1 it would only constrain scheduling).
-        if constexpr (MT == 1) __asm__ volatile("" ::: "memory");
       }
     }
     if constexpr (ROWS) {
