@@ -26,9 +26,9 @@ sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
 DEFAULT_PLANS = {  # (plan, waves, seqs, mode, channels per workgroup) per (L, io)
-    (128, "fp32"): ("16x16", 12, 2, 1, 3), (128, "bf16"): ("16x16", 12, 2, 1, 3),
-    (256, "fp32"): ("32x16", 12, 2, 1, 3), (256, "bf16"): ("32x16", 12, 2, 1, 3),
-    (512, "fp32"): ("32x32", 12, 2, 1, 3), (512, "bf16"): ("32x32", 12, 2, 1, 3),
+    (128, "fp32"): ("16x16", 4, 2, 1, 1), (128, "bf16"): ("16x16", 4, 2, 1, 1),
+    (256, "fp32"): ("32x16", 4, 2, 1, 1), (256, "bf16"): ("32x16", 4, 2, 1, 1),
+    (512, "fp32"): ("32x32", 4, 2, 1, 1), (512, "bf16"): ("32x32", 4, 2, 1, 1),
     (1024, "fp32"): ("64x32", 12, 2, 1, 3), (1024, "bf16"): ("64x32", 12, 2, 1, 3),
     (2048, "fp32"): ("64x64", 12, 2, 1, 3), (2048, "bf16"): ("64x64", 12, 2, 1, 3),
     (4096, "fp32"): ("32x16x16", 8, 2, 0, 1), (4096, "bf16"): ("32x16x16", 8, 2, 0, 1),
