@@ -25,16 +25,6 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
-DEFAULT_PLANS = {  # (plan, waves, seqs, mode, channels per workgroup) per (L, io)
-    (128, "fp32"): ("16x16", 4, 2, 1, 1), (128, "bf16"): ("16x16", 4, 2, 1, 1),
-    (256, "fp32"): ("32x16", 4, 2, 1, 1), (256, "bf16"): ("32x16", 4, 2, 1, 1),
-    (512, "fp32"): ("32x32", 4, 2, 1, 1), (512, "bf16"): ("32x32", 4, 2, 1, 1),
-    (1024, "fp32"): ("64x32", 12, 2, 1, 3), (1024, "bf16"): ("64x32", 12, 2, 1, 3),
-    (2048, "fp32"): ("64x64", 12, 2, 1, 3), (2048, "bf16"): ("64x64", 12, 2, 1, 3),
-    (4096, "fp32"): ("32x16x16", 8, 2, 0, 1), (4096, "bf16"): ("32x16x16", 8, 2, 0, 1),
-    (8192, "fp32"): ("32x32x16", 4, 2, 0, 1), (8192, "bf16"): ("64x16x16", 8, 2, 0, 1),
-    (16384, "fp32"): ("32x32x32", 8, 1, 0, 1), (16384, "bf16"): ("32x32x32", 8, 2, 0, 1),
-}
 
 
 def parse():
@@ -127,7 +117,8 @@ def main():
 
     dev = torch.device("cuda:0")
     B, H, L, io = a.B, a.H, a.L, a.io
-    spec, waves, seqs, mode, channels = DEFAULT_PLANS[(L, io)]
+    base = sf.default_plan(L, io, B, acc=a.acc)
+    spec, waves, seqs, mode, channels = base.name(), base.waves, base.seqs, base.mode, base.channels
     if a.plan:
         spec = a.plan
     if a.waves:

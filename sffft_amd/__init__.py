@@ -142,6 +142,33 @@ def make_plan(spec: str, waves: int, acc: int = 0, cached: int = 1, seqs: int = 
     return Plan(r[0], r[1], r[2], waves, acc, cached, seqs, mode, channels)
 
 
+# Tuned plan per (L, I/O) at B=8, H=768 (spec, waves, seqs, mode, channels): wave plans up to
+# L=2048, workgroup plans beyond. fp32 I/O at L=16384 keeps one sequence per transform: two
+# measure at the 5e-4 bound.
+DEFAULT_PLANS = {
+    (128, "fp32"): ("16x16", 4, 2, 1, 1), (128, "bf16"): ("16x16", 4, 2, 1, 1),
+    (256, "fp32"): ("32x16", 4, 2, 1, 1), (256, "bf16"): ("32x16", 4, 2, 1, 1),
+    (512, "fp32"): ("32x32", 4, 2, 1, 1), (512, "bf16"): ("32x32", 4, 2, 1, 1),
+    (1024, "fp32"): ("64x32", 12, 2, 1, 3), (1024, "bf16"): ("64x32", 12, 2, 1, 3),
+    (2048, "fp32"): ("64x64", 12, 2, 1, 3), (2048, "bf16"): ("64x64", 12, 2, 1, 3),
+    (4096, "fp32"): ("32x16x16", 8, 2, 0, 1), (4096, "bf16"): ("32x16x16", 8, 2, 0, 1),
+    (8192, "fp32"): ("32x32x16", 4, 2, 0, 1), (8192, "bf16"): ("64x16x16", 8, 2, 0, 1),
+    (16384, "fp32"): ("32x32x32", 8, 1, 0, 1), (16384, "bf16"): ("32x32x32", 8, 2, 0, 1),
+}
+# One sequence per transform (workgroup kernel) for an odd batch
+ODD_BATCH_PLANS = {128: ("16x16", 2), 256: ("32x16", 2), 512: ("32x32", 2), 1024: ("64x32", 4),
+                   2048: ("16x16x16", 8), 4096: ("32x16x16", 8), 8192: ("32x32x16", 4), 16384: ("32x32x32", 8)}
+
+
+def default_plan(L: int, io: str = "fp32", B: int = 8, acc: int = 0) -> Plan:
+    """The tuned plan for length L and I/O type; pairs of sequences need an even B."""
+    spec, waves, seqs, mode, channels = DEFAULT_PLANS[(L, io)]
+    if seqs == 2 and B % 2:
+        spec, waves = ODD_BATCH_PLANS[L]
+        seqs, mode, channels = 1, 0, 1
+    return make_plan(spec, waves, acc=acc, cached=1, seqs=seqs, mode=mode, channels=channels)
+
+
 def plan_check(L: int, plan: Plan) -> int:
     return lib().sffft_plan_check(L, ctypes.byref(plan))
 

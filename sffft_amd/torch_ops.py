@@ -1,0 +1,139 @@
+"""PyTorch operators over the C ABI of libsffft.so.
+
+The reference names a library with a PyTorch binding as its next step (README.md:177), for the
+long-convolution layers of Hyena/H3/S4-style models (README.md:11). This module provides it:
+
+- ``torch.ops.sffft.spectrum(k, plan)``: the kernel-order spectrum [H, 2L] complex64 of a real
+  filter k [H, L] (fp32);
+- ``torch.ops.sffft.conv(u, kf, plan)``: y = causal_conv(u, k) for u [B, H, L] fp32 or bf16;
+- ``LongConv``: the two together, with the spectrum cached per (filter tensor, its version, L,
+  plan), so a layer whose filter does not change computes the spectrum once.
+
+``plan`` is the list of the nine ``sffft_plan`` fields (``plan_fields``). Both operators have fake
+(meta) implementations, so they trace under ``torch.compile`` and ``torch.export``, and they are
+plain stream-ordered launches, so they capture into CUDA/HIP graphs.
+
+Gradients: ``conv`` is differentiable in u. Causal convolution's adjoint is the anti-causal
+correlation du[m] = sum_{n >= m} dy[n] k[n - m], which is flip(causal_conv(flip(dy), k)), so the
+backward pass runs the same kernel on the same spectrum. The filter gradient (a reduction over
+the batch) is not provided: ``spectrum`` raises if its filter requires grad.
+"""
+from __future__ import annotations
+
+import weakref
+from typing import List, Optional, Sequence
+
+import torch
+
+from . import Plan, conv as _conv, default_plan, spectrum as _spectrum
+
+PLAN_FIELDS = ("r0", "r1", "r2", "waves", "acc", "cached", "seqs", "mode", "channels")
+
+
+def plan_fields(plan: Plan) -> List[int]:
+    """The plan as the integer list the operators take."""
+    return [int(getattr(plan, f)) for f in PLAN_FIELDS]
+
+
+def _plan(fields: Sequence[int]) -> Plan:
+    if len(fields) != len(PLAN_FIELDS):
+        raise ValueError(f"a plan has {len(PLAN_FIELDS)} fields {PLAN_FIELDS}, got {len(fields)}")
+    return Plan(*[int(x) for x in fields])
+
+
+@torch.library.custom_op("sffft::spectrum", mutates_args=(), device_types="cuda")
+def spectrum(k: torch.Tensor, plan: List[int]) -> torch.Tensor:
+    """Kernel-order spectrum of the real filters k [H, L] fp32 for the given plan."""
+    return _spectrum(k, k.shape[1], _plan(plan))
+
+
+@spectrum.register_fake
+def _spectrum_fake(k, plan):
+    torch._check(k.dim() == 2, lambda: "k must be [H, L]")
+    torch._check(k.dtype == torch.float32, lambda: "k must be float32")
+    return k.new_empty((k.shape[0], 2 * k.shape[1]), dtype=torch.complex64)
+
+
+def _no_filter_grad(ctx, grad):
+    raise RuntimeError("sffft::spectrum has no gradient with respect to the filter")
+
+
+def _spectrum_setup(ctx, inputs, output):
+    pass
+
+
+spectrum.register_autograd(_no_filter_grad, setup_context=_spectrum_setup)
+
+
+@torch.library.custom_op("sffft::conv", mutates_args=(), device_types="cuda")
+def conv(u: torch.Tensor, kf: torch.Tensor, plan: List[int]) -> torch.Tensor:
+    """y[b, h, n] = sum_{m <= n} u[b, h, m] k[h, n - m] for u [B, H, L] fp32 or bf16 and kf
+    from ``spectrum`` with the same plan."""
+    return _conv(u, kf, _plan(plan))
+
+
+@conv.register_fake
+def _conv_fake(u, kf, plan):
+    torch._check(u.dim() == 3, lambda: "u must be [B, H, L]")
+    torch._check(u.dtype in (torch.float32, torch.bfloat16), lambda: "u must be float32 or bfloat16")
+    torch._check(kf.dim() == 2 and kf.shape[0] == u.shape[1] and kf.shape[1] == 2 * u.shape[2],
+                 lambda: "kf must be [H, 2L]")
+    return torch.empty_like(u)
+
+
+def _conv_setup(ctx, inputs, output):
+    _, kf, plan = inputs
+    ctx.save_for_backward(kf)
+    ctx.plan = list(plan)
+
+
+def _conv_backward(ctx, dy):
+    (kf,) = ctx.saved_tensors
+    du = None
+    if ctx.needs_input_grad[0]:
+        du = torch.ops.sffft.conv(dy.flip(-1).contiguous(), kf, ctx.plan).flip(-1)
+    return du, None, None
+
+
+conv.register_autograd(_conv_backward, setup_context=_conv_setup)
+
+
+class LongConv:
+    """Causal long convolution y = causal_conv(u, k) with the filter spectrum cached.
+
+    The spectrum of a filter tensor is kept while the tensor lives and is recomputed when it is
+    modified in place (its version counter moves) or when L or the plan changes. With no plan
+    given, the tuned plan for (L, dtype, B) is used.
+    """
+
+    def __init__(self, plan: Optional[Plan] = None):
+        self.plan = plan
+        # id(filter) -> (weak reference to it, (version, shape, plan), spectrum); an entry is
+        # dropped when its filter is freed (tensors compare elementwise, so they cannot key a
+        # WeakKeyDictionary)
+        self._cache: dict = {}
+        self.spectra_computed = 0
+
+    def plan_for(self, u: torch.Tensor) -> Plan:
+        if self.plan is not None:
+            return self.plan
+        io = "bf16" if u.dtype == torch.bfloat16 else "fp32"
+        return default_plan(u.shape[-1], io, u.shape[0])
+
+    def spectrum(self, k: torch.Tensor, plan: Plan) -> torch.Tensor:
+        fields = plan_fields(plan)
+        key = (k._version, tuple(k.shape), tuple(fields))
+        hit = self._cache.get(id(k))
+        same = hit is not None and hit[0]() is k
+        if same and hit[1] == key:
+            return hit[2]
+        kf = torch.ops.sffft.spectrum(k, fields)
+        if not same:
+            weakref.finalize(k, self._cache.pop, id(k), None)
+        self._cache[id(k)] = (weakref.ref(k), key, kf)
+        self.spectra_computed += 1
+        return kf
+
+    def __call__(self, u: torch.Tensor, k: torch.Tensor) -> torch.Tensor:
+        plan = self.plan_for(u)
+        return torch.ops.sffft.conv(u, self.spectrum(k, plan), plan_fields(plan))

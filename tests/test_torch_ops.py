@@ -1,0 +1,162 @@
+"""The PyTorch operators over the C ABI (sffft_amd/torch_ops.py).
+
+CPU: schemas, fake-tensor shape propagation, the tuned default plans, and the identity behind
+the input gradient (the adjoint of causal convolution is flip o causal_conv o flip), checked on
+the fp64 oracle against a brute-force anti-causal correlation.
+GPU: bit equality with the C-ABI path, torch.library.opcheck, the gradient against the oracle,
+the spectrum cache, torch.compile and graph capture.
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+import sffft_amd as sf
+from sffft_amd import torch_ops
+
+
+def test_schemas():
+    assert str(torch.ops.sffft.conv.default._schema) == "sffft::conv(Tensor u, Tensor kf, SymInt[] plan) -> Tensor"
+    assert str(torch.ops.sffft.spectrum.default._schema) == "sffft::spectrum(Tensor k, SymInt[] plan) -> Tensor"
+
+
+def test_fake_shapes():
+    from torch._subclasses.fake_tensor import FakeTensorMode
+
+    p = torch_ops.plan_fields(sf.default_plan(1024))
+    with FakeTensorMode():
+        k = torch.empty(768, 1024, device="cuda")
+        kf = torch.ops.sffft.spectrum(k, p)
+        y = torch.ops.sffft.conv(torch.empty(8, 768, 1024, device="cuda", dtype=torch.bfloat16), kf, p)
+        assert kf.shape == (768, 2048) and kf.dtype == torch.complex64
+        assert y.shape == (8, 768, 1024) and y.dtype == torch.bfloat16
+
+
+@pytest.mark.parametrize("L", sf.LENGTHS)
+def test_default_plans_are_compiled(L):
+    for io in ("fp32", "bf16"):
+        for B in (8, 7):
+            p = sf.default_plan(L, io, B)
+            assert sf.plan_check(L, p) == 0, (L, io, B, p)
+            assert B % p.seqs == 0
+
+
+def test_adjoint_is_flipped_causal_convolution():
+    rng = np.random.default_rng(3)
+    B, H, L = 2, 3, 64
+    dy = rng.standard_normal((B, H, L)).astype(np.float32)
+    k = rng.standard_normal((H, L)).astype(np.float32)
+    # brute force: du[b,h,m] = sum_{n >= m} dy[b,h,n] k[h,n-m]
+    du = np.zeros((B, H, L))
+    for m in range(L):
+        for n in range(m, L):
+            du[:, :, m] += dy[:, :, n].astype(np.float64) * k[None, :, n - m]
+    got = oracle.direct_conv(dy[:, :, ::-1].copy(), k)[:, :, ::-1]
+    assert np.abs(got - du).max() < 1e-9 * np.abs(du).max()
+    # a plausible mistake (no output flip) fails the same check
+    wrong = oracle.direct_conv(dy[:, :, ::-1].copy(), k)
+    assert np.abs(wrong - du).max() > 1e-3 * np.abs(du).max()
+
+
+# ---- GPU ----------------------------------------------------------------------------------
+
+def _inputs(dev, B, H, L, seed):
+    u, k = oracle.gen_inputs(B, H, L, seed=seed)
+    return torch.from_numpy(u).to(dev), torch.from_numpy(k).to(dev), u, k
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("L,io", [(1024, "fp32"), (4096, "bf16")])
+def test_ops_match_the_c_abi(dev, L, io):
+    u, k, _, _ = _inputs(dev, 4, 13, L, seed=L)
+    if io == "bf16":
+        u = u.to(torch.bfloat16)
+    plan = sf.default_plan(L, io, 4)
+    p = torch_ops.plan_fields(plan)
+    kf = torch.ops.sffft.spectrum(k, p)
+    assert torch.equal(torch.view_as_real(kf), torch.view_as_real(sf.spectrum(k, L, plan)))
+    assert torch.equal(torch.ops.sffft.conv(u, kf, p), sf.conv(u, kf, plan))
+
+
+@pytest.mark.gpu
+def test_opcheck(dev):
+    u, k, _, _ = _inputs(dev, 2, 3, 256, seed=1)
+    p = torch_ops.plan_fields(sf.default_plan(256, "fp32", 2))
+    kf = torch.ops.sffft.spectrum(k, p)
+    torch.library.opcheck(torch.ops.sffft.spectrum.default, (k, p))
+    torch.library.opcheck(torch.ops.sffft.conv.default, (u, kf, p))
+    torch.library.opcheck(torch.ops.sffft.conv.default, (u.clone().requires_grad_(), kf, p))
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("L", [512, 4096])
+def test_input_gradient(dev, L):
+    B, H = 4, 5
+    u, k, _, k_np = _inputs(dev, B, H, L, seed=11)
+    w = torch.randn(B, H, L, device=dev, generator=torch.Generator(device=dev).manual_seed(2))
+    lc = torch_ops.LongConv()
+    u.requires_grad_()
+    (lc(u, k) * w).sum().backward()
+    # du[b,h,m] = sum_{n>=m} w[b,h,n] k[h,n-m], in fp64
+    w_np = w.cpu().numpy()
+    ref = oracle.conv(w_np[:, :, ::-1].copy(), k_np)[:, :, ::-1]
+    err = oracle.rel_l2(u.grad.cpu().numpy(), ref)
+    print(f"L={L} input-gradient rel_l2={err:.3e}", flush=True)
+    assert err <= 6e-4
+
+
+@pytest.mark.gpu
+def test_no_filter_gradient(dev):
+    u, k, _, _ = _inputs(dev, 2, 3, 256, seed=4)
+    k.requires_grad_()
+    y = torch_ops.LongConv()(u, k)
+    with pytest.raises(RuntimeError, match="no gradient"):
+        y.sum().backward()
+
+
+@pytest.mark.gpu
+def test_spectrum_cache(dev):
+    u, k, _, _ = _inputs(dev, 2, 3, 1024, seed=5)
+    lc = torch_ops.LongConv()
+    y1 = lc(u, k)
+    y2 = lc(u, k)
+    assert lc.spectra_computed == 1 and torch.equal(y1, y2)
+    k.mul_(2.0)  # in place: the version moves, the spectrum is recomputed
+    y3 = lc(u, k)
+    assert lc.spectra_computed == 2
+    assert torch.allclose(y3, 2 * y1, rtol=0, atol=1e-5 * float(y1.abs().max()))
+    k2 = k.clone()
+    lc(u, k2)
+    assert lc.spectra_computed == 3
+
+
+@pytest.mark.gpu
+def test_torch_compile(dev):
+    u, k, _, _ = _inputs(dev, 2, 6, 512, seed=6)
+    p = torch_ops.plan_fields(sf.default_plan(512, "fp32", 2))
+
+    def f(u, k):
+        return torch.ops.sffft.conv(u * 2.0, torch.ops.sffft.spectrum(k, p), p)
+
+    eager = f(u, k)
+    compiled = torch.compile(f, fullgraph=True, backend="aot_eager")(u, k)
+    assert torch.equal(compiled, eager)
+
+
+@pytest.mark.gpu
+def test_graph_capture(dev):
+    u, k, _, _ = _inputs(dev, 4, 6, 1024, seed=7)
+    p = torch_ops.plan_fields(sf.default_plan(1024, "fp32", 4))
+    kf = torch.ops.sffft.spectrum(k, p)
+    eager = torch.ops.sffft.conv(u, kf, p)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        y = torch.ops.sffft.conv(u, kf, p)
+    for i in range(3):
+        y.zero_()
+        torch.ops.sffft.conv(u * 0.5, kf, p)  # eager work between replays
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(y, eager), i
