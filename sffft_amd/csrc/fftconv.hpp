@@ -71,6 +71,12 @@ struct Plan {
   static constexpr int PLANE0 = S == 3 ? cmax(R0 * ROW, M * PB) : cmax(R0 * PA, R1 * PB);
   static constexpr int PLANE = (PLANE0 + 63) & ~63;
   static constexpr int LDS_BYTES = 2 * PLANE * 2;
+  // Column of k0 group c4 (a multiple of 4) in row block mt of the [m][k0] plane:
+  // three-stage plans write it swizzled with the 16-row block's index m / R2 (phase2_s3).
+  __device__ static int s3_col(int mt, int c4) {
+    if constexpr (S == 3) return c4 ^ (4 * (((16 * mt) / R2) & (R0 / 4 - 1)));
+    else return c4;
+  }
   static_assert(R0 >= 16 && R1 >= 16 && (S == 2 || R2 >= 16), "radices are 16, 32 or 64");
   static_assert(R0 <= 64 && R1 <= 64 && R2 <= 64, "radices are 16, 32 or 64");
 };
@@ -279,9 +285,12 @@ __device__ __forceinline__ void phase1(const P1Data<P, NW, NSEQ>& d, _Float16* r
           *reinterpret_cast<h4*>(im + pos) = to_h4(xi);
         } else {
 #pragma unroll
-          for (int v = 0; v < 4; v++) {  // [k0][n2][n1]
+          for (int v = 0; v < 4; v++) {  // [k0][n2 ^ (k0 & 15)][n1]
+            // The 16 lanes of this scalar write differ in k0, i.e. by whole ROW pitches
+            // (multiples of the bank count): swizzling the row index with k0 spreads
+            // them over 16 rows and banks. phase2_s3 reads the row back swizzled.
             const int m = 16 * mt + 4 * g + v, n1 = m / P::R2, n2 = m % P::R2;
-            const int pos = k0 * P::ROW + n2 * P::PA + n1;
+            const int pos = k0 * P::ROW + (n2 ^ (k0 & 15)) * P::PA + n1;
             re[pos] = (_Float16)xr[v];
             im[pos] = (_Float16)xi[v];
           }
@@ -433,7 +442,8 @@ __device__ __forceinline__ void phase2_s3(_Float16* re, _Float16* im, const floa
 #pragma unroll
       for (int t2 = 0; t2 < T2; t2++)
 #pragma unroll
-        for (int ks = 0; ks < T1; ks++) a[t2][ks] = lds_frag(re, im, rb + (16 * t2 + c) * P::PA + 16 * ks + 4 * g);
+        for (int ks = 0; ks < T1; ks++)
+          a[t2][ks] = lds_frag(re, im, rb + (16 * t2 + (c ^ (k0 & 15))) * P::PA + 16 * ks + 4 * g);
 #pragma unroll
       for (int t2 = 0; t2 < T2; t2++) {
 #pragma unroll
@@ -547,11 +557,15 @@ __device__ __forceinline__ void phase2_s3(_Float16* re, _Float16* im, const floa
     for (int t2 = 0; t2 < T2; t2++)
 #pragma unroll
       for (int nt = 0; nt < T1; nt++) {
+        // The 16 lanes of this scalar write differ in m by R2 rows (multiples of the
+        // bank count): the k0 column is swizzled in groups of 4 with the lane's row
+        // block, k0 ^ 4*(c mod R0/4), which phase3 undoes (P::s3_col).
         const int m0 = (16 * nt + c) * R2 + 16 * t2 + 4 * g;
+        const int col = k0 ^ (4 * (c & (R0 / 4 - 1)));
 #pragma unroll
         for (int v = 0; v < 4; v++) {
-          re[(m0 + v) * P::PB + k0] = outr[i][t2][nt][v];
-          im[(m0 + v) * P::PB + k0] = outi[i][t2][nt][v];
+          re[(m0 + v) * P::PB + col] = outr[i][t2][nt][v];
+          im[(m0 + v) * P::PB + col] = outi[i][t2][nt][v];
         }
       }
   }
@@ -598,7 +612,7 @@ __device__ __forceinline__ void phase3(TIO* __restrict__ ya, TIO* __restrict__ y
   };
   auto load = [&](int mt, h8* a) {
 #pragma unroll
-    for (int ks = 0; ks < KS; ks++) a[ks] = lds_frag(re, im, (16 * mt + r) * P::PB + 16 * ks + 4 * g);
+    for (int ks = 0; ks < KS; ks++) a[ks] = lds_frag(re, im, (16 * mt + r) * P::PB + P::s3_col(mt, 16 * ks + 4 * g));
   };
   if constexpr (MT >= NW) {
     for (int mt = wave; mt < MT; mt += NW) {
