@@ -657,7 +657,9 @@ __global__ void __launch_bounds__(64 * NW)
   __shared__ __attribute__((aligned(16))) _Float16 lds[2 * P::PLANE];
   _Float16* re = lds;
   _Float16* im = lds + P::PLANE;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  // the wavefront index is uniform: a scalar register, so the work split derived from
+  // it runs on the scalar unit
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   int h, bp;
   block_to_item(blockIdx.x, H, B / NSEQ, h, bp);
   const size_t row_a = ((size_t)(bp * NSEQ) * H + h) * P::L;

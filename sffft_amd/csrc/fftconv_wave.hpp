@@ -3,7 +3,9 @@
 // One 64-lane wavefront carries one pair of sequences of one channel -- packed as
 // the real and imaginary parts of a single complex transform -- through every
 // stage of the forward transform, the spectrum product and the inverse transform
-// without leaving VGPRs: no LDS transposes and no barriers between stages.
+// in VGPRs: no LDS exchange and no barrier between stages. Only the pair's input
+// and output pass through a per-wavefront LDS scratch, so that global memory is
+// read and written in whole rows.
 //
 // Why it works (v_mfma_f32_16x16x32_f16, complex K interleave of fftconv.hpp):
 // a result tile D[i][j] sits in lane (j, g) as rows i = 4g..4g+3; an operand
@@ -506,7 +508,9 @@ __global__ void __launch_bounds__(64 * NW)
   float4* TW2 = P::TW_TABLES == 2 ? TW1 + P::TW_F4 : TW1;
   float4* SPL = lds + P::TAB_F4;
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  // the wavefront index is uniform: read it into a scalar register so the pair and
+  // channel arithmetic derived from it runs on the scalar unit
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   TIO* S = reinterpret_cast<TIO*>(lds + P::TAB_F4 + SPL_F4 + wave * SCR_F4);
   const int BP = B >> 1, h0 = blockIdx.x * CH;
   const int nch = H - h0 < CH ? H - h0 : CH;  // channels of this workgroup
