@@ -428,9 +428,28 @@ __device__ __forceinline__ void phase2_s3(_Float16* re, _Float16* im, const floa
   constexpr float sc2 = R2 == 16 ? 0.25f : R2 == 32 ? 0.17677669529663687f : 0.125f;
   const int c = lane & 15, g = lane >> 4;
   h4 outr[ROWS][T2][T1], outi[ROWS][T2][T1];
+  // Twiddles of the stage over n1 and of the inverse over k2 do not depend on the row:
+  // w^(R0 (16nt + c)(16t + 4g + v)), the same values for both when R1 == R2. With one
+  // tile per axis they are evaluated once per wavefront instead of twice per row.
+  constexpr bool SHARED_TW = T1 == 1 && T2 == 1;
+  float twr[4], twi[4];
+  if constexpr (SHARED_TW) twiddle4<N>(R0 * c, 4 * g, 1.f, twr, twi);
+  auto tw_n1 = [&](int nt, int t2, float sc, float* wr, float* wi) {
+    if constexpr (SHARED_TW) {
+#pragma unroll
+      for (int v = 0; v < 4; v++) {
+        wr[v] = sc * twr[v];
+        wi[v] = sc * twi[v];
+      }
+    } else {
+      twiddle4<N>(R0 * (16 * nt + c), 16 * t2 + 4 * g, sc, wr, wi);
+    }
+  };
 #pragma unroll
   for (int i = 0; i < ROWS; i++) {
-    const int k0 = wave + i * NW;
+    // each wavefront owns ROWS consecutive rows, so the final [m][k0] write stores
+    // consecutive k0 of one m as one vector
+    const int k0 = wave * ROWS + i;
     const int rb = k0 * P::ROW;
     float4 kq[T1][T2][2];  // this row's spectrum, in flight while the stage over n1 runs
 #pragma unroll
@@ -457,7 +476,7 @@ __device__ __forceinline__ void phase2_s3(_Float16* re, _Float16* im, const floa
           dr = round_acc(dr, acc16);
           di = round_acc(di, acc16);
           float wr[4], wi[4], xr[4], xi[4];
-          twiddle4<N>(R0 * (16 * nt + c), 16 * t2 + 4 * g, sc1, wr, wi);
+          tw_n1(nt, t2, sc1, wr, wi);
 #pragma unroll
           for (int v = 0; v < 4; v++) {
             xr[v] = dr[v] * wr[v] - di[v] * wi[v];
@@ -504,7 +523,7 @@ __device__ __forceinline__ void phase2_s3(_Float16* re, _Float16* im, const floa
           er = round_acc(er, acc16);
           ei = round_acc(ei, acc16);
           float wr[4], wi[4], xr[4], xi[4];
-          twiddle4<N>(R0 * (16 * nt + c), 16 * t1 + 4 * g, sc2, wr, wi);
+          tw_n1(nt, t1, sc2, wr, wi);
 #pragma unroll
           for (int v = 0; v < 4; v++) {
             xr[v] = er[v] * wr[v] - ei[v] * wi[v];
@@ -550,25 +569,43 @@ __device__ __forceinline__ void phase2_s3(_Float16* re, _Float16* im, const floa
     wave_sync();
   }
   __syncthreads();  // every row has been read before the [m][k0] layout is written
+  // [m][k0]: the wavefront's ROWS consecutive k0 of one m are written as one vector
+  // (up to 4 halves). The 16 lanes of a write differ in m by R2 rows (multiples of
+  // the bank count), so the k0 column is swizzled in groups of 4 with the lane's row
+  // block, k0 ^ 4*(c mod R0/4), which phase3 undoes (P::s3_col).
+  constexpr int G = ROWS < 4 ? ROWS : 4;
 #pragma unroll
-  for (int i = 0; i < ROWS; i++) {
-    const int k0 = wave + i * NW;
+  for (int t2 = 0; t2 < T2; t2++)
 #pragma unroll
-    for (int t2 = 0; t2 < T2; t2++)
+    for (int nt = 0; nt < T1; nt++) {
+      const int m0 = (16 * nt + c) * R2 + 16 * t2 + 4 * g;
 #pragma unroll
-      for (int nt = 0; nt < T1; nt++) {
-        // The 16 lanes of this scalar write differ in m by R2 rows (multiples of the
-        // bank count): the k0 column is swizzled in groups of 4 with the lane's row
-        // block, k0 ^ 4*(c mod R0/4), which phase3 undoes (P::s3_col).
-        const int m0 = (16 * nt + c) * R2 + 16 * t2 + 4 * g;
-        const int col = k0 ^ (4 * (c & (R0 / 4 - 1)));
+      for (int q = 0; q < ROWS / G; q++) {
+        const int col = (wave * ROWS + q * G) ^ (4 * (c & (R0 / 4 - 1)));
 #pragma unroll
         for (int v = 0; v < 4; v++) {
-          re[(m0 + v) * P::PB + col] = outr[i][t2][nt][v];
-          im[(m0 + v) * P::PB + col] = outi[i][t2][nt][v];
+          _Float16 hr[G], hi[G];
+#pragma unroll
+          for (int j = 0; j < G; j++) {
+            hr[j] = outr[q * G + j][t2][nt][v];
+            hi[j] = outi[q * G + j][t2][nt][v];
+          }
+          _Float16* pr = re + (m0 + v) * P::PB + col;
+          _Float16* pi = im + (m0 + v) * P::PB + col;
+          if constexpr (G == 4) {
+            *reinterpret_cast<h4*>(pr) = (h4){hr[0], hr[1], hr[2], hr[3]};
+            *reinterpret_cast<h4*>(pi) = (h4){hi[0], hi[1], hi[2], hi[3]};
+          } else if constexpr (G == 2) {
+            typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+            *reinterpret_cast<h2*>(pr) = (h2){hr[0], hr[1]};
+            *reinterpret_cast<h2*>(pi) = (h2){hi[0], hi[1]};
+          } else {
+            *pr = hr[0];
+            *pi = hi[0];
+          }
         }
       }
-  }
+    }
 }
 
 // ---- Phase 3: last inverse stage over k0, first L outputs only -----------------
