@@ -99,6 +99,15 @@ __device__ __forceinline__ uint16_t f32_to_bf16(float f) {
 }
 
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+// Four fp32 values as four bf16 in two dwords, round to nearest even: the gfx950
+// packed conversion, two values per instruction (f32_to_bf16 costs six per value).
+__device__ __forceinline__ u32x2 f4_to_bf16x4(f4 v) {
+  typedef float fl2 __attribute__((ext_vector_type(2)));
+  typedef __bf16 bf2 __attribute__((ext_vector_type(2)));
+  const bf2 lo = __builtin_convertvector((fl2){v[0], v[1]}, bf2);
+  const bf2 hi = __builtin_convertvector((fl2){v[2], v[3]}, bf2);
+  return (u32x2){__builtin_bit_cast(uint32_t, lo), __builtin_bit_cast(uint32_t, hi)};
+}
 // fp16-accumulation mode: the raw tile accumulator is rounded to fp16 (range and
 // rounding of an fp16 accumulator; +-inf beyond 65504).
 __device__ __forceinline__ f4 round_acc(f4 v, int acc16) {
@@ -563,6 +572,10 @@ __device__ __forceinline__ void phase2_s3(_Float16* re, _Float16* im, const floa
           }
           outr[i][t2][nt] = to_h4(xr);
           outi[i][t2][nt] = to_h4(xi);
+          // With one tile per axis, computed here rather than sunk to the final write,
+          // which would keep every row's accumulators and twiddle live to the end
+          // (measured: faster with one tile per axis, slower with more).
+          if constexpr (T1 * T2 == 1) asm volatile("" : "+v"(outr[i][t2][nt]), "+v"(outi[i][t2][nt]));
         }
       }
     }
@@ -637,13 +650,8 @@ __device__ __forceinline__ void phase3(TIO* __restrict__ ya, TIO* __restrict__ y
         *reinterpret_cast<f4*>(ya + o) = zr * sc0;
         if constexpr (NSEQ == 2) *reinterpret_cast<f4*>(yb + o) = zi * -sc0;
       } else {
-        *reinterpret_cast<u32x2*>(ya + o) =
-            (u32x2){(uint32_t)f32_to_bf16(zr[0] * sc0) | ((uint32_t)f32_to_bf16(zr[1] * sc0) << 16),
-                    (uint32_t)f32_to_bf16(zr[2] * sc0) | ((uint32_t)f32_to_bf16(zr[3] * sc0) << 16)};
-        if constexpr (NSEQ == 2)
-          *reinterpret_cast<u32x2*>(yb + o) =
-              (u32x2){(uint32_t)f32_to_bf16(-zi[0] * sc0) | ((uint32_t)f32_to_bf16(-zi[1] * sc0) << 16),
-                      (uint32_t)f32_to_bf16(-zi[2] * sc0) | ((uint32_t)f32_to_bf16(-zi[3] * sc0) << 16)};
+        *reinterpret_cast<u32x2*>(ya + o) = f4_to_bf16x4(zr * sc0);
+        if constexpr (NSEQ == 2) *reinterpret_cast<u32x2*>(yb + o) = f4_to_bf16x4(zi * -sc0);
       }
     }
   };

@@ -124,13 +124,7 @@ __device__ __forceinline__ float4 ld_f4(const float4* p) { return *p; }
 // Per-lane output pieces (plans without the operand scratch): plain write-back
 // stores, so L2 merges the partial lines before they reach HBM.
 __device__ __forceinline__ void store4(float* p, f4 v) { *reinterpret_cast<f4*>(p) = v; }
-__device__ __forceinline__ void store4(uint16_t* p, f4 v) {
-  typedef float fl2 __attribute__((ext_vector_type(2)));
-  typedef __bf16 bf2 __attribute__((ext_vector_type(2)));
-  const bf2 lo = __builtin_convertvector((fl2){v[0], v[1]}, bf2);  // round to nearest even
-  const bf2 hi = __builtin_convertvector((fl2){v[2], v[3]}, bf2);
-  *reinterpret_cast<u32x2*>(p) = (u32x2){__builtin_bit_cast(uint32_t, lo), __builtin_bit_cast(uint32_t, hi)};
-}
+__device__ __forceinline__ void store4(uint16_t* p, f4 v) { *reinterpret_cast<u32x2*>(p) = f4_to_bf16x4(v); }
 
 // 16-byte blocks copied from global memory straight into LDS (global_load_lds_dwordx4:
 // lane i of the wave writes bytes [16i, 16i+16) after the wave-uniform LDS base).
@@ -332,13 +326,7 @@ __device__ __forceinline__ void pair_operands(const PairLoads<P, TIO, true>& d, 
 // (streaming stores of partial lines would reach HBM as partial writes).
 // Rows from ROWS3 on (the zero half of R0 = 16) are not stored.
 __device__ __forceinline__ void put4(float* p, f4 v) { *reinterpret_cast<f4*>(p) = v; }
-__device__ __forceinline__ void put4(uint16_t* p, f4 v) {
-  typedef float fl2 __attribute__((ext_vector_type(2)));
-  typedef __bf16 bf2 __attribute__((ext_vector_type(2)));
-  const bf2 lo = __builtin_convertvector((fl2){v[0], v[1]}, bf2);  // round to nearest even
-  const bf2 hi = __builtin_convertvector((fl2){v[2], v[3]}, bf2);
-  *reinterpret_cast<u32x2*>(p) = (u32x2){__builtin_bit_cast(uint32_t, lo), __builtin_bit_cast(uint32_t, hi)};
-}
+__device__ __forceinline__ void put4(uint16_t* p, f4 v) { *reinterpret_cast<u32x2*>(p) = f4_to_bf16x4(v); }
 
 template <class P, class TIO>
 __device__ __forceinline__ void store_rows(TIO* S, const f4 (&z)[P::MT], TIO* __restrict__ y, int lane) {
