@@ -213,48 +213,47 @@ struct P1Split {
   __device__ static int nt(int wave, int j) { return BY_MT ? j : wave / MT + j * WPM; }
 };
 
-template <class P, int NW, int NSEQ>
+// The raw input elements of this wave's phase-1 A tiles: lane (r, g) of tile i holds
+// row m = 16 mt + r at the 8 (NSEQ = 1) or 4 + 4 (NSEQ = 2) first-digit positions n0 of
+// its K slots; positions in the zero-padded half (n0 >= R0/2) are not loaded.
+template <class P, int NW, int NSEQ, class TIO>
 struct P1Data {
-  h8 a[P1Split<P, NW, NSEQ>::TPW][P1Split<P, NW, NSEQ>::KS];
+  TIO raw[P1Split<P, NW, NSEQ>::TPW][P1Split<P, NW, NSEQ>::KS][8];
 };
 
-template <class P, int NSEQ, class TIO>
-__device__ __forceinline__ void p1_load(const TIO* __restrict__ xa, const TIO* __restrict__ xb, int mt,
-                                        h8* a, int r, int g) {
-  constexpr int R0 = P::R0, M = P::M;
-  constexpr int KS = NSEQ == 2 ? (R0 / 2 + 15) / 16 : 1;
-  const int m = 16 * mt + r;
-#pragma unroll
-  for (int ks = 0; ks < KS; ks++) {
-#pragma unroll
-    for (int j = 0; j < 8; j++) {
-      int n0;
-      const TIO* src;
-      if constexpr (NSEQ == 2) {
-        n0 = 16 * ks + 4 * g + (j & 3);
-        src = j < 4 ? xa : xb;
-      } else {
-        n0 = j < 4 ? 4 * g + j : 16 + 4 * g + (j - 4);
-        src = xa;
-      }
-      float v = 0.f;
-      if (n0 < R0 / 2) v = io_to_f32(src[n0 * M + m]);
-      a[ks][j] = (_Float16)v;
-    }
-  }
+template <class P, int NSEQ>
+__device__ __forceinline__ int p1_n0(int ks, int g, int j) {
+  if constexpr (NSEQ == 2) return 16 * ks + 4 * g + (j & 3);
+  else return j < 4 ? 4 * g + j : 16 + 4 * g + (j - 4);
 }
 
-// Issues every input load of this wave's phase-1 tiles (one HBM round trip).
+// Issues every input load of this wave's phase-1 tiles (one HBM round trip). The
+// elements stay raw until their tile is computed, and the compiler barrier keeps all
+// loads ahead of the first tile: converted here, or sunk to their use, the later
+// tiles' loads would be issued only after the first tile's have landed.
 template <class P, int NW, int NSEQ, class TIO>
 __device__ __forceinline__ void p1_prefetch(const TIO* __restrict__ xa, const TIO* __restrict__ xb,
-                                            P1Data<P, NW, NSEQ>& d, int lane, int wave) {
+                                            P1Data<P, NW, NSEQ, TIO>& d, int lane, int wave) {
   using SP = P1Split<P, NW, NSEQ>;
+  constexpr int R0 = P::R0, M = P::M;
+  const int r = lane & 15, g = lane >> 4;
 #pragma unroll
-  for (int i = 0; i < SP::TPW; i++) p1_load<P, NSEQ, TIO>(xa, xb, SP::mt(wave, i), d.a[i], lane & 15, lane >> 4);
+  for (int i = 0; i < SP::TPW; i++) {
+    const int m = 16 * SP::mt(wave, i) + r;
+#pragma unroll
+    for (int ks = 0; ks < SP::KS; ks++)
+#pragma unroll
+      for (int j = 0; j < 8; j++) {
+        const int n0 = p1_n0<P, NSEQ>(ks, g, j);
+        const TIO* src = NSEQ == 2 && j >= 4 ? xb : xa;
+        d.raw[i][ks][j] = n0 < R0 / 2 ? src[n0 * M + m] : TIO(0);
+      }
+  }
+  asm volatile("" ::: "memory");
 }
 
-template <class P, int NW, int NSEQ, bool CACHED>
-__device__ __forceinline__ void phase1(const P1Data<P, NW, NSEQ>& d, _Float16* re, _Float16* im,
+template <class P, int NW, int NSEQ, class TIO, bool CACHED>
+__device__ __forceinline__ void phase1(const P1Data<P, NW, NSEQ, TIO>& d, _Float16* re, _Float16* im,
                                        const h8* __restrict__ ftab, int acc16, int lane, int wave) {
   using SP = P1Split<P, NW, NSEQ>;
   constexpr int R0 = P::R0, N = P::N, KS = SP::KS;
@@ -263,6 +262,11 @@ __device__ __forceinline__ void phase1(const P1Data<P, NW, NSEQ>& d, _Float16* r
 #pragma unroll
   for (int i = 0; i < SP::TPW; i++) {
     const int mt = SP::mt(wave, i);
+    h8 a[KS];
+#pragma unroll
+    for (int ks = 0; ks < KS; ks++)
+#pragma unroll
+      for (int j = 0; j < 8; j++) a[ks][j] = (_Float16)io_to_f32(d.raw[i][ks][j]);
 #pragma unroll
     for (int j = 0; j < SP::NTW; j++) {
       const int nt = SP::nt(wave, j);
@@ -271,11 +275,11 @@ __device__ __forceinline__ void phase1(const P1Data<P, NW, NSEQ>& d, _Float16* r
 #pragma unroll
         for (int ks = 0; ks < KS; ks++) {
           if constexpr (NSEQ == 2) {
-            dr = mfma(d.a[i][ks], cf_frag<R0, CACHED>(ftab, nt, ks, 0, lane), dr);
-            di = mfma(d.a[i][ks], cf_frag<R0, CACHED>(ftab, nt, ks, 1, lane), di);
+            dr = mfma(a[ks], cf_frag<R0, CACHED>(ftab, nt, ks, 0, lane), dr);
+            di = mfma(a[ks], cf_frag<R0, CACHED>(ftab, nt, ks, 1, lane), di);
           } else {
-            dr = mfma(d.a[i][ks], ri_frag<R0, CACHED>(ftab, nt, 0, lane), dr);
-            di = mfma(d.a[i][ks], ri_frag<R0, CACHED>(ftab, nt, 1, lane), di);
+            dr = mfma(a[ks], ri_frag<R0, CACHED>(ftab, nt, 0, lane), dr);
+            di = mfma(a[ks], ri_frag<R0, CACHED>(ftab, nt, 1, lane), di);
           }
         }
         dr = round_acc(dr, acc16);
@@ -454,17 +458,30 @@ __device__ __forceinline__ void phase2_s3(_Float16* re, _Float16* im, const floa
       twiddle4<N>(R0 * (16 * nt + c), 16 * t2 + 4 * g, sc, wr, wi);
     }
   };
+  // A row's spectrum (kernel order, 2 KB per tile) is read from L2 while the row
+  // before it is computed: with one tile per axis the loads are issued one row ahead
+  // (double-buffered); otherwise at the start of their own row, in flight while the
+  // stage over n1 runs.
+  constexpr int KQB = T1 * T2 == 1 && ROWS > 1 ? 2 : 1;
+  float4 kq[KQB][T1][T2][2];
+  auto load_row_spectrum = [&](int k0, float4 (*q)[T2][2]) {
+#pragma unroll
+    for (int t1 = 0; t1 < T1; t1++)
+#pragma unroll
+      for (int mt = 0; mt < T2; mt++) load_k4(K + (size_t)((k0 * T1 + t1) * T2 + mt) * 256, lane, q[t1][mt]);
+  };
+  if constexpr (KQB == 2) load_row_spectrum(wave * ROWS, kq[0]);
 #pragma unroll
   for (int i = 0; i < ROWS; i++) {
     // each wavefront owns ROWS consecutive rows, so the final [m][k0] write stores
     // consecutive k0 of one m as one vector
     const int k0 = wave * ROWS + i;
     const int rb = k0 * P::ROW;
-    float4 kq[T1][T2][2];  // this row's spectrum, in flight while the stage over n1 runs
-#pragma unroll
-    for (int t1 = 0; t1 < T1; t1++)
-#pragma unroll
-      for (int mt = 0; mt < T2; mt++) load_k4(K + (size_t)((k0 * T1 + t1) * T2 + mt) * 256, lane, kq[t1][mt]);
+    if constexpr (KQB == 2) {
+      if (i + 1 < ROWS) load_row_spectrum(k0 + 1, kq[(i + 1) & 1]);
+    } else {
+      load_row_spectrum(k0, kq[0]);
+    }
     {  // stage over n1: [n2][n1] -> [k1][n2]
       h8 a[T2][T1];
 #pragma unroll
@@ -520,7 +537,7 @@ __device__ __forceinline__ void phase2_s3(_Float16* re, _Float16* im, const floa
           di[mt] = round_acc(di[mt], acc16);
         }
         h8 a2[T2];
-        spectrum_product<T2>(dr, di, kq[t1], a2);
+        spectrum_product<T2>(dr, di, kq[KQB == 2 ? i & 1 : 0][t1], a2);
 #pragma unroll
         for (int nt = 0; nt < T2; nt++) {
           f4 er = {0.f, 0.f, 0.f, 0.f}, ei = {0.f, 0.f, 0.f, 0.f};
@@ -712,16 +729,16 @@ __global__ void __launch_bounds__(64 * NW)
   const float2* K = kf + (size_t)h * P::N;
   // every global load of the input (and, for two-stage plans, of the spectrum) is
   // issued before any computation, so their latencies overlap
-  P1Data<P, NW, NSEQ> ad;
+  P1Data<P, NW, NSEQ, TIO> ad;
   p1_prefetch<P, NW, NSEQ, TIO>(u + row_a, u + row_b, ad, lane, wave);
   if constexpr (P::S == 2) {
     KData2<P, NW> kd;
     k_prefetch_s2<P, NW>(K, kd, lane, wave);
-    phase1<P, NW, NSEQ, CACHED>(ad, re, im, ftab, acc16, lane, wave);
+    phase1<P, NW, NSEQ, TIO, CACHED>(ad, re, im, ftab, acc16, lane, wave);
     __syncthreads();
     phase2_s2<P, NW, CACHED>(re, im, kd, ftab, acc16, lane, wave);
   } else {
-    phase1<P, NW, NSEQ, CACHED>(ad, re, im, ftab, acc16, lane, wave);
+    phase1<P, NW, NSEQ, TIO, CACHED>(ad, re, im, ftab, acc16, lane, wave);
     __syncthreads();
     phase2_s3<P, NW, CACHED>(re, im, K, ftab, acc16, lane, wave);
   }
