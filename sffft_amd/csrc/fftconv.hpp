@@ -37,6 +37,17 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+// fp16 operands of fp32-I/O three-stage plans that also carry their fp16 remainder
+// (x = hi + lo, the contraction run on both: ~22 significant bits instead of 11, for
+// twice that contraction's MFMAs). Bit 3: the input of the first stage; bits 0, 1, 2:
+// the operands of the stage over n2, the inverse over k2 (the spectrum product) and the
+// inverse over k1. Measured at B=8 H=768 with pairs of sequences per transform: the
+// input split (8) takes rel-L2 from 4.7e-4..5.1e-4 to 4.2e-4..4.7e-4 for 3-5% time;
+// all four (15) reach 3.3e-4..3.7e-4 for 22-41%.
+#ifndef SFFFT_FP32_SPLITS
+#define SFFFT_FP32_SPLITS 8
+#endif
+
 namespace sffft {
 
 typedef _Float16 h4 __attribute__((ext_vector_type(4)));
@@ -118,6 +129,15 @@ __device__ __forceinline__ f4 round_acc(f4 v, int acc16) {
   return v;
 }
 
+// -1 in a register the compiler cannot see through: fma(-1, (float)h, x) with a known
+// -1 becomes x - (float)h, three instructions (convert, subtract, convert) instead of
+// one mixed-precision fma.
+__device__ __forceinline__ float minus_one() {
+  float m = -1.f;
+  asm volatile("" : "+v"(m));
+  return m;
+}
+
 // ---- DFT fragments ------------------------------------------------------------
 template <int R, bool CACHED>
 __device__ __forceinline__ h8 cf_frag(const h8* __restrict__ ftab, int a, int b, int kind, int lane) {
@@ -155,13 +175,15 @@ __device__ __forceinline__ h8 ri_frag(const h8* __restrict__ ftab, int nt, int k
   }
 }
 
-// w[v] = sc * exp(-2*pi*i * a*(b0+v) / N), v = 0..3 (src/sffft.cu:106-113 for the
-// exponent; the angle is reduced to (-1/2, 1/2] revolutions before v_sin/v_cos).
+// w[v] = sc * exp(-2*pi*i * (e0 + step*v) / N), v = 0..3 (src/sffft.cu:106-113 for the
+// exponent): the base from v_sin/v_cos with the angle reduced to (-1/2, 1/2]
+// revolutions (e/N is exact), the others by a complex recurrence.
 template <int N>
-__device__ __forceinline__ void twiddle4(int a, int b0, float sc, float* wr, float* wi) {
-  const int e0 = (a * b0) & (N - 1), e1 = a & (N - 1);
+__device__ __forceinline__ void twiddle4e(int e0, int step, float sc, float* wr, float* wi) {
+  e0 &= N - 1;
+  step &= N - 1;
   const float x0 = (float)(e0 > N / 2 ? e0 - N : e0) * (1.0f / N);
-  const float x1 = (float)(e1 > N / 2 ? e1 - N : e1) * (1.0f / N);
+  const float x1 = (float)(step > N / 2 ? step - N : step) * (1.0f / N);
   float r = sc * cos_rev(x0), i = -sc * sin_rev(x0);
   const float sr = cos_rev(x1), si = -sin_rev(x1);
   wr[0] = r;
@@ -174,6 +196,11 @@ __device__ __forceinline__ void twiddle4(int a, int b0, float sc, float* wr, flo
     wr[v] = r;
     wi[v] = i;
   }
+}
+// w[v] = sc * exp(-2*pi*i * a*(b0+v) / N)
+template <int N>
+__device__ __forceinline__ void twiddle4(int a, int b0, float sc, float* wr, float* wi) {
+  twiddle4e<N>(a * b0, a, sc, wr, wi);
 }
 
 // 8-half operand: slots 0..3 from the real plane, 4..7 from the imaginary plane.
@@ -252,36 +279,44 @@ __device__ __forceinline__ void p1_prefetch(const TIO* __restrict__ xa, const TI
   asm volatile("" ::: "memory");
 }
 
-template <class P, int NW, int NSEQ, class TIO, bool CACHED>
+// SPLIT_IN: the fp32 input enters the first stage as fp16 value plus fp16 remainder
+// (twice that stage's MFMAs), so it is not rounded to 11 bits there.
+template <class P, int NW, int NSEQ, class TIO, bool CACHED, bool SPLIT_IN>
 __device__ __forceinline__ void phase1(const P1Data<P, NW, NSEQ, TIO>& d, _Float16* re, _Float16* im,
                                        const h8* __restrict__ ftab, int acc16, int lane, int wave) {
   using SP = P1Split<P, NW, NSEQ>;
-  constexpr int R0 = P::R0, N = P::N, KS = SP::KS;
+  constexpr int R0 = P::R0, N = P::N, KS = SP::KS, SI = SPLIT_IN ? 1 : 0;
   constexpr float sc0 = R0 == 16 ? 0.25f : R0 == 32 ? 0.17677669529663687f : 0.125f;
   const int r = lane & 15, g = lane >> 4;
 #pragma unroll
   for (int i = 0; i < SP::TPW; i++) {
     const int mt = SP::mt(wave, i);
-    h8 a[KS];
+    h8 a[KS][1 + SI];
 #pragma unroll
     for (int ks = 0; ks < KS; ks++)
 #pragma unroll
-      for (int j = 0; j < 8; j++) a[ks][j] = (_Float16)io_to_f32(d.raw[i][ks][j]);
+      for (int j = 0; j < 8; j++) {
+        const float x = io_to_f32(d.raw[i][ks][j]);
+        a[ks][0][j] = (_Float16)x;
+        if constexpr (SPLIT_IN) a[ks][SI][j] = (_Float16)__builtin_fmaf(minus_one(), (float)a[ks][0][j], x);
+      }
 #pragma unroll
     for (int j = 0; j < SP::NTW; j++) {
       const int nt = SP::nt(wave, j);
       if (nt < SP::NT) {
         f4 dr = {0.f, 0.f, 0.f, 0.f}, di = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int ks = 0; ks < KS; ks++) {
-          if constexpr (NSEQ == 2) {
-            dr = mfma(a[ks], cf_frag<R0, CACHED>(ftab, nt, ks, 0, lane), dr);
-            di = mfma(a[ks], cf_frag<R0, CACHED>(ftab, nt, ks, 1, lane), di);
-          } else {
-            dr = mfma(a[ks], ri_frag<R0, CACHED>(ftab, nt, 0, lane), dr);
-            di = mfma(a[ks], ri_frag<R0, CACHED>(ftab, nt, 1, lane), di);
+        for (int ks = 0; ks < KS; ks++)
+#pragma unroll
+          for (int p = 0; p <= SI; p++) {
+            if constexpr (NSEQ == 2) {
+              dr = mfma(a[ks][p], cf_frag<R0, CACHED>(ftab, nt, ks, 0, lane), dr);
+              di = mfma(a[ks][p], cf_frag<R0, CACHED>(ftab, nt, ks, 1, lane), di);
+            } else {
+              dr = mfma(a[ks][p], ri_frag<R0, CACHED>(ftab, nt, 0, lane), dr);
+              di = mfma(a[ks][p], ri_frag<R0, CACHED>(ftab, nt, 1, lane), di);
+            }
           }
-        }
         dr = round_acc(dr, acc16);
         di = round_acc(di, acc16);
         const int k0 = 16 * nt + r;
@@ -323,8 +358,13 @@ __device__ __forceinline__ void load_k4(const float2* __restrict__ kp, int lane,
 }
 // d = forward result tiles D[kk][c] (lane column c, rows 16*mt+4g+v), q = spectrum
 // tiles. Returns A operands conj(D*K)^T for the inverse.
-template <int T>
-__device__ __forceinline__ void spectrum_product(const f4* dr, const f4* di, const float4 (*q)[2], h8* a2) {
+// With SPLIT, lo receives the fp16 remainders x - (float)hi: the inverse stage that
+// follows runs on hi and on lo (twice the MFMAs of that stage), so the product enters
+// it with about 22 significant bits instead of 11. One fp16 rounding of the five of a
+// three-stage plan (three of a two-stage one) is removed this way.
+template <int T, bool SPLIT = false>
+__device__ __forceinline__ void spectrum_product(const f4* dr, const f4* di, const float4 (*q)[2], h8* a2,
+                                                 h8* lo = nullptr) {
 #pragma unroll
   for (int mt = 0; mt < T; mt++) {
     const float4 k01 = q[mt][0], k23 = q[mt][1];
@@ -336,6 +376,10 @@ __device__ __forceinline__ void spectrum_product(const f4* dr, const f4* di, con
       const float xi = dr[mt][v] * ki[v] + di[mt][v] * kr[v];
       a2[mt][v] = (_Float16)xr;
       a2[mt][4 + v] = (_Float16)(-xi);
+      if constexpr (SPLIT) {  // x - hi as one v_fma_mix each
+        lo[mt][v] = (_Float16)__builtin_fmaf(minus_one(), (float)a2[mt][v], xr);
+        lo[mt][4 + v] = (_Float16)__builtin_fmaf(minus_one(), (float)a2[mt][4 + v], -xi);
+      }
     }
   }
 }
@@ -361,7 +405,7 @@ __device__ __forceinline__ void k_prefetch_s2(const float2* __restrict__ K, KDat
   }
 }
 
-template <class P, int NW, bool CACHED>
+template <class P, int NW, bool CACHED, bool SPLIT>
 __device__ __forceinline__ void phase2_s2(_Float16* re, _Float16* im, const KData2<P, NW>& kd,
                                           const h8* __restrict__ ftab, int acc16, int lane, int wave) {
   constexpr int R0 = P::R0, R1 = P::R1, N = P::N, ST = R0 / 16, T1 = R1 / 16;
@@ -389,8 +433,8 @@ __device__ __forceinline__ void phase2_s2(_Float16* re, _Float16* im, const KDat
         dr[mt] = round_acc(dr[mt], acc16);
         di[mt] = round_acc(di[mt], acc16);
       }
-      h8 a2[T1];
-      spectrum_product<T1>(dr, di, kd.q[i], a2);
+      h8 a2[T1], a2lo[SPLIT ? T1 : 1];
+      spectrum_product<T1, SPLIT>(dr, di, kd.q[i], a2, a2lo);
 #pragma unroll
       for (int nt = 0; nt < T1; nt++) {
         f4 er = {0.f, 0.f, 0.f, 0.f}, ei = {0.f, 0.f, 0.f, 0.f};
@@ -398,6 +442,10 @@ __device__ __forceinline__ void phase2_s2(_Float16* re, _Float16* im, const KDat
         for (int mt = 0; mt < T1; mt++) {
           er = mfma(a2[mt], cf_frag<R1, CACHED>(ftab, nt, mt, 0, lane), er);
           ei = mfma(a2[mt], cf_frag<R1, CACHED>(ftab, nt, mt, 1, lane), ei);
+          if constexpr (SPLIT) {
+            er = mfma(a2lo[mt], cf_frag<R1, CACHED>(ftab, nt, mt, 0, lane), er);
+            ei = mfma(a2lo[mt], cf_frag<R1, CACHED>(ftab, nt, mt, 1, lane), ei);
+          }
         }
         er = round_acc(er, acc16);
         ei = round_acc(ei, acc16);
@@ -429,21 +477,48 @@ __device__ __forceinline__ void phase2_s2(_Float16* re, _Float16* im, const KDat
 }
 
 // ---- Phase 2, three-stage plans: per k0 row, stages over n1 and n2, spectrum,
-// inverse over k2 and k1. A row is owned by one wave; only wave-level ordering
-// is needed until the final [m][k0] write.
-template <class P, int NW, bool CACHED>
+// inverse over k2 and k1 (src/sffft.cu:273-279). A row is owned by one wavefront and
+// all its stages run in registers: the result tile of each contraction has the lane
+// layout of the next one's B operand (lane (c, g) holds rows 4g..4g+3 of column c,
+// and a B operand holds K indices 4g..4g+3 of column c):
+//   stage over n1:  D[n2][k1]  = A[n2][n1] (LDS, [k0][n2][n1]) x F1,  then twiddle
+//   stage over n2:  D2[k2][k1] = F2 x D          (D as B, K = n2)
+//   spectrum:       A2[k1][k2] = conj(D2 K)^T    (the result lanes, read as A)
+//   inverse k2:     E[n2][k1]^T = A2 x F2,  i.e. E[k1][n2] with n2 on the lane column;
+//                   twiddle, then E as B (K = k1) of
+//   inverse k1:     Z[n1][n2]  = F1 x E,  last twiddle w^(k0 m), m = n1 R2 + n2.
+// Every operand is rounded to fp16 once. SPLITS (bits 0..2 of SFFFT_FP32_SPLITS for
+// fp32 I/O) selects the operands made here in registers that also carry their fp16
+// remainder, the contraction then running on both parts.
+template <bool SPLIT>
+__device__ __forceinline__ void pack_operand(const float* xr, const float* xi, h8& hi, h8& lo) {
+#pragma unroll
+  for (int v = 0; v < 4; v++) {
+    hi[v] = (_Float16)xr[v];
+    hi[4 + v] = (_Float16)xi[v];
+    if constexpr (SPLIT) {  // x - hi as one v_fma_mix each (hi read as fp16, times -1)
+      lo[v] = (_Float16)__builtin_fmaf(minus_one(), (float)hi[v], xr[v]);
+      lo[4 + v] = (_Float16)__builtin_fmaf(minus_one(), (float)hi[4 + v], xi[v]);
+    }
+  }
+}
+
+template <class P, int NW, bool CACHED, int SPLITS>
 __device__ __forceinline__ void phase2_s3(_Float16* re, _Float16* im, const float2* __restrict__ K,
                                           const h8* __restrict__ ftab, int acc16, int lane, int wave) {
   constexpr int R0 = P::R0, R1 = P::R1, R2 = P::R2, N = P::N, T1 = R1 / 16, T2 = R2 / 16;
   constexpr int ROWS = R0 / NW;
+  constexpr int SB = SPLITS & 1, SE = (SPLITS >> 2) & 1;
+  constexpr bool SA = (SPLITS >> 1) & 1;
   static_assert(R0 % NW == 0, "three-stage plans need R0 divisible by the wave count");
   constexpr float sc1 = R1 == 16 ? 0.25f : R1 == 32 ? 0.17677669529663687f : 0.125f;
   constexpr float sc2 = R2 == 16 ? 0.25f : R2 == 32 ? 0.17677669529663687f : 0.125f;
   const int c = lane & 15, g = lane >> 4;
-  h4 outr[ROWS][T2][T1], outi[ROWS][T2][T1];
-  // Twiddles of the stage over n1 and of the inverse over k2 do not depend on the row:
-  // w^(R0 (16nt + c)(16t + 4g + v)), the same values for both when R1 == R2. With one
-  // tile per axis they are evaluated once per wavefront instead of twice per row.
+  h4 outr[ROWS][T1][T2], outi[ROWS][T1][T2];  // [row][n1 tile][n2 tile]
+  // The twiddles after the stage over n1 and after the inverse over k2 do not depend on
+  // the row: w^(R0 k1 n2) at (k1, n2) = (16nt + c, 16t + 4g + v) and (16t + 4g + v, 16nt + c),
+  // the same values when R1 == R2. With one tile per axis they are evaluated once per
+  // wavefront instead of twice per row.
   constexpr bool SHARED_TW = T1 == 1 && T2 == 1;
   float twr[4], twi[4];
   if constexpr (SHARED_TW) twiddle4<N>(R0 * c, 4 * g, 1.f, twr, twi);
@@ -456,6 +531,13 @@ __device__ __forceinline__ void phase2_s3(_Float16* re, _Float16* im, const floa
       }
     } else {
       twiddle4<N>(R0 * (16 * nt + c), 16 * t2 + 4 * g, sc, wr, wi);
+    }
+  };
+  auto twiddle = [](const f4& er, const f4& ei, const float* wr, const float* wi, float* xr, float* xi) {
+#pragma unroll
+    for (int v = 0; v < 4; v++) {
+      xr[v] = er[v] * wr[v] - ei[v] * wi[v];
+      xi[v] = er[v] * wi[v] + ei[v] * wr[v];
     }
   };
   // A row's spectrum (kernel order, 2 KB per tile) is read from L2 while the row
@@ -482,7 +564,9 @@ __device__ __forceinline__ void phase2_s3(_Float16* re, _Float16* im, const floa
     } else {
       load_row_spectrum(k0, kq[0]);
     }
-    {  // stage over n1: [n2][n1] -> [k1][n2]
+    // stage over n1: A[n2][n1] from the row's [n2 ^ (k0 & 15)][n1] block
+    h8 b[T1][T2][1 + SB];  // [k1 tile][n2 tile][hi, lo]: B operands of the stage over n2
+    {
       h8 a[T2][T1];
 #pragma unroll
       for (int t2 = 0; t2 < T2; t2++)
@@ -503,125 +587,104 @@ __device__ __forceinline__ void phase2_s3(_Float16* re, _Float16* im, const floa
           di = round_acc(di, acc16);
           float wr[4], wi[4], xr[4], xi[4];
           tw_n1(nt, t2, sc1, wr, wi);
-#pragma unroll
-          for (int v = 0; v < 4; v++) {
-            xr[v] = dr[v] * wr[v] - di[v] * wi[v];
-            xi[v] = dr[v] * wi[v] + di[v] * wr[v];
-          }
-          const int pos = rb + (16 * nt + c) * P::PC + 16 * t2 + 4 * g;
-          *reinterpret_cast<h4*>(re + pos) = to_h4(xr);
-          *reinterpret_cast<h4*>(im + pos) = to_h4(xi);
+          twiddle(dr, di, wr, wi, xr, xi);
+          pack_operand<SB != 0>(xr, xi, b[nt][t2][0], b[nt][t2][SB]);
         }
       }
     }
-    wave_sync();
-    {  // stage over n2, spectrum, inverse over k2: [k1][n2] -> conj, [n2][k1]
-      h8 b[T1][T2];
+    // stage over n2, spectrum, inverse over k2
+    h8 e[T2][T1][1 + SE];  // [n2 tile][k1 tile][hi, lo]: B operands of the inverse over k1
 #pragma unroll
-      for (int t1 = 0; t1 < T1; t1++)
+    for (int t1 = 0; t1 < T1; t1++) {
+      f4 dr[T2], di[T2];
 #pragma unroll
-        for (int ks = 0; ks < T2; ks++) b[t1][ks] = lds_frag(re, im, rb + (16 * t1 + c) * P::PC + 16 * ks + 4 * g);
+      for (int mt = 0; mt < T2; mt++) {
+        dr[mt] = (f4){0.f, 0.f, 0.f, 0.f};
+        di[mt] = (f4){0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int t1 = 0; t1 < T1; t1++) {
-        f4 dr[T2], di[T2];
+        for (int ks = 0; ks < T2; ks++)
+#pragma unroll
+          for (int p = 0; p <= SB; p++) {
+            dr[mt] = mfma(cf_frag<R2, CACHED>(ftab, mt, ks, 0, lane), b[t1][ks][p], dr[mt]);
+            di[mt] = mfma(cf_frag<R2, CACHED>(ftab, mt, ks, 1, lane), b[t1][ks][p], di[mt]);
+          }
+        dr[mt] = round_acc(dr[mt], acc16);
+        di[mt] = round_acc(di[mt], acc16);
+      }
+      h8 a2[T2], a2lo[SA ? T2 : 1];
+      spectrum_product<T2, SA>(dr, di, kq[KQB == 2 ? i & 1 : 0][t1], a2, a2lo);
+#pragma unroll
+      for (int nt = 0; nt < T2; nt++) {
+        f4 er = {0.f, 0.f, 0.f, 0.f}, ei = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int mt = 0; mt < T2; mt++) {
-          dr[mt] = (f4){0.f, 0.f, 0.f, 0.f};
-          di[mt] = (f4){0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-          for (int ks = 0; ks < T2; ks++) {
-            dr[mt] = mfma(cf_frag<R2, CACHED>(ftab, mt, ks, 0, lane), b[t1][ks], dr[mt]);
-            di[mt] = mfma(cf_frag<R2, CACHED>(ftab, mt, ks, 1, lane), b[t1][ks], di[mt]);
+          er = mfma(a2[mt], cf_frag<R2, CACHED>(ftab, nt, mt, 0, lane), er);
+          ei = mfma(a2[mt], cf_frag<R2, CACHED>(ftab, nt, mt, 1, lane), ei);
+          if constexpr (SA) {
+            er = mfma(a2lo[mt], cf_frag<R2, CACHED>(ftab, nt, mt, 0, lane), er);
+            ei = mfma(a2lo[mt], cf_frag<R2, CACHED>(ftab, nt, mt, 1, lane), ei);
           }
-          dr[mt] = round_acc(dr[mt], acc16);
-          di[mt] = round_acc(di[mt], acc16);
         }
-        h8 a2[T2];
-        spectrum_product<T2>(dr, di, kq[KQB == 2 ? i & 1 : 0][t1], a2);
-#pragma unroll
-        for (int nt = 0; nt < T2; nt++) {
-          f4 er = {0.f, 0.f, 0.f, 0.f}, ei = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-          for (int mt = 0; mt < T2; mt++) {
-            er = mfma(a2[mt], cf_frag<R2, CACHED>(ftab, nt, mt, 0, lane), er);
-            ei = mfma(a2[mt], cf_frag<R2, CACHED>(ftab, nt, mt, 1, lane), ei);
-          }
-          er = round_acc(er, acc16);
-          ei = round_acc(ei, acc16);
-          float wr[4], wi[4], xr[4], xi[4];
-          tw_n1(nt, t1, sc2, wr, wi);
-#pragma unroll
-          for (int v = 0; v < 4; v++) {
-            xr[v] = er[v] * wr[v] - ei[v] * wi[v];
-            xi[v] = er[v] * wi[v] + ei[v] * wr[v];
-          }
-          const int pos = rb + (16 * nt + c) * P::PA + 16 * t1 + 4 * g;
-          *reinterpret_cast<h4*>(re + pos) = to_h4(xr);
-          *reinterpret_cast<h4*>(im + pos) = to_h4(xi);
-        }
+        er = round_acc(er, acc16);
+        ei = round_acc(ei, acc16);
+        float wr[4], wi[4], xr[4], xi[4];
+        tw_n1(nt, t1, sc2, wr, wi);
+        twiddle(er, ei, wr, wi, xr, xi);
+        pack_operand<SE != 0>(xr, xi, e[nt][t1][0], e[nt][t1][SE]);
       }
     }
-    wave_sync();
-    {  // inverse over k1: [n2][k1] -> staged, written as [m][k0]
-      h8 a[T2][T1];
+    // inverse over k1 and the last twiddle
 #pragma unroll
-      for (int t2 = 0; t2 < T2; t2++)
+    for (int nt = 0; nt < T2; nt++) {
 #pragma unroll
-        for (int ks = 0; ks < T1; ks++) a[t2][ks] = lds_frag(re, im, rb + (16 * t2 + c) * P::PA + 16 * ks + 4 * g);
+      for (int mt = 0; mt < T1; mt++) {
+        f4 zr = {0.f, 0.f, 0.f, 0.f}, zi = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int t2 = 0; t2 < T2; t2++) {
+        for (int ks = 0; ks < T1; ks++)
 #pragma unroll
-        for (int nt = 0; nt < T1; nt++) {
-          f4 er = {0.f, 0.f, 0.f, 0.f}, ei = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-          for (int ks = 0; ks < T1; ks++) {
-            er = mfma(a[t2][ks], cf_frag<R1, CACHED>(ftab, nt, ks, 0, lane), er);
-            ei = mfma(a[t2][ks], cf_frag<R1, CACHED>(ftab, nt, ks, 1, lane), ei);
+          for (int p = 0; p <= SE; p++) {
+            zr = mfma(cf_frag<R1, CACHED>(ftab, mt, ks, 0, lane), e[nt][ks][p], zr);
+            zi = mfma(cf_frag<R1, CACHED>(ftab, mt, ks, 1, lane), e[nt][ks][p], zi);
           }
-          er = round_acc(er, acc16);
-          ei = round_acc(ei, acc16);
-          float wr[4], wi[4], xr[4], xi[4];
-          twiddle4<N>(k0, (16 * nt + c) * R2 + 16 * t2 + 4 * g, sc1, wr, wi);
-#pragma unroll
-          for (int v = 0; v < 4; v++) {
-            xr[v] = er[v] * wr[v] - ei[v] * wi[v];
-            xi[v] = er[v] * wi[v] + ei[v] * wr[v];
-          }
-          outr[i][t2][nt] = to_h4(xr);
-          outi[i][t2][nt] = to_h4(xi);
-          // With one tile per axis, computed here rather than sunk to the final write,
-          // which would keep every row's accumulators and twiddle live to the end
-          // (measured: faster with one tile per axis, slower with more).
-          if constexpr (T1 * T2 == 1) asm volatile("" : "+v"(outr[i][t2][nt]), "+v"(outi[i][t2][nt]));
-        }
+        zr = round_acc(zr, acc16);
+        zi = round_acc(zi, acc16);
+        // lane value v is n1 = 16mt + 4g + v, n2 = 16nt + c: m = n1 R2 + n2
+        float wr[4], wi[4], xr[4], xi[4];
+        twiddle4e<N>(k0 * ((16 * mt + 4 * g) * R2 + 16 * nt + c), k0 * R2, sc1, wr, wi);
+        twiddle(zr, zi, wr, wi, xr, xi);
+        outr[i][mt][nt] = to_h4(xr);
+        outi[i][mt][nt] = to_h4(xi);
+        // With one tile per axis, computed here rather than sunk to the final write,
+        // which would keep every row's accumulators and twiddle live to the end
+        // (measured: faster with one tile per axis, slower with more).
+        if constexpr (T1 * T2 == 1) asm volatile("" : "+v"(outr[i][mt][nt]), "+v"(outi[i][mt][nt]));
       }
     }
-    wave_sync();
   }
   __syncthreads();  // every row has been read before the [m][k0] layout is written
   // [m][k0]: the wavefront's ROWS consecutive k0 of one m are written as one vector
-  // (up to 4 halves). The 16 lanes of a write differ in m by R2 rows (multiples of
-  // the bank count), so the k0 column is swizzled in groups of 4 with the lane's row
-  // block, k0 ^ 4*(c mod R0/4), which phase3 undoes (P::s3_col).
+  // (up to 4 halves). The k0 column is swizzled in groups of 4 with the row's n1 =
+  // m / R2, k0 ^ 4*(n1 mod R0/4), which phase3 undoes (P::s3_col): rows R2 apart (a
+  // multiple of the bank count) then fall on different banks.
   constexpr int G = ROWS < 4 ? ROWS : 4;
 #pragma unroll
-  for (int t2 = 0; t2 < T2; t2++)
+  for (int mt = 0; mt < T1; mt++)
 #pragma unroll
-    for (int nt = 0; nt < T1; nt++) {
-      const int m0 = (16 * nt + c) * R2 + 16 * t2 + 4 * g;
+    for (int nt = 0; nt < T2; nt++)
 #pragma unroll
-      for (int q = 0; q < ROWS / G; q++) {
-        const int col = (wave * ROWS + q * G) ^ (4 * (c & (R0 / 4 - 1)));
+      for (int v = 0; v < 4; v++) {
+        const int n1 = 16 * mt + 4 * g + v, m = n1 * R2 + 16 * nt + c;
 #pragma unroll
-        for (int v = 0; v < 4; v++) {
+        for (int q = 0; q < ROWS / G; q++) {
+          const int col = (wave * ROWS + q * G) ^ (4 * (n1 & (R0 / 4 - 1)));
           _Float16 hr[G], hi[G];
 #pragma unroll
           for (int j = 0; j < G; j++) {
-            hr[j] = outr[q * G + j][t2][nt][v];
-            hi[j] = outi[q * G + j][t2][nt][v];
+            hr[j] = outr[q * G + j][mt][nt][v];
+            hi[j] = outi[q * G + j][mt][nt][v];
           }
-          _Float16* pr = re + (m0 + v) * P::PB + col;
-          _Float16* pi = im + (m0 + v) * P::PB + col;
+          _Float16* pr = re + m * P::PB + col;
+          _Float16* pi = im + m * P::PB + col;
           if constexpr (G == 4) {
             *reinterpret_cast<h4*>(pr) = (h4){hr[0], hr[1], hr[2], hr[3]};
             *reinterpret_cast<h4*>(pi) = (h4){hi[0], hi[1], hi[2], hi[3]};
@@ -635,7 +698,6 @@ __device__ __forceinline__ void phase2_s3(_Float16* re, _Float16* im, const floa
           }
         }
       }
-    }
 }
 
 // ---- Phase 3: last inverse stage over k0, first L outputs only -----------------
@@ -734,13 +796,14 @@ __global__ void __launch_bounds__(64 * NW)
   if constexpr (P::S == 2) {
     KData2<P, NW> kd;
     k_prefetch_s2<P, NW>(K, kd, lane, wave);
-    phase1<P, NW, NSEQ, TIO, CACHED>(ad, re, im, ftab, acc16, lane, wave);
+    phase1<P, NW, NSEQ, TIO, CACHED, false>(ad, re, im, ftab, acc16, lane, wave);
     __syncthreads();
-    phase2_s2<P, NW, CACHED>(re, im, kd, ftab, acc16, lane, wave);
+    phase2_s2<P, NW, CACHED, sizeof(TIO) == 4>(re, im, kd, ftab, acc16, lane, wave);
   } else {
-    phase1<P, NW, NSEQ, TIO, CACHED>(ad, re, im, ftab, acc16, lane, wave);
+    phase1<P, NW, NSEQ, TIO, CACHED, sizeof(TIO) == 4 && (SFFFT_FP32_SPLITS & 8)>(ad, re, im, ftab, acc16, lane,
+                                                                                   wave);
     __syncthreads();
-    phase2_s3<P, NW, CACHED>(re, im, K, ftab, acc16, lane, wave);
+    phase2_s3<P, NW, CACHED, sizeof(TIO) == 4 ? SFFFT_FP32_SPLITS : 0>(re, im, K, ftab, acc16, lane, wave);
   }
   __syncthreads();
   phase3<P, NW, NSEQ, TIO, CACHED>(y + row_a, y + row_b, re, im, ftab, acc16, lane, wave);
