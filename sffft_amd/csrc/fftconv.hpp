@@ -175,6 +175,32 @@ __device__ __forceinline__ h8 ri_frag(const h8* __restrict__ ftab, int nt, int k
   }
 }
 
+// The complex DFT fragments of radix R for a loop over rows: evaluated once and held
+// in registers (HOLD), or produced at each use. Held fragments pass through an empty
+// asm so the compiler neither re-evaluates them per row nor sinks them into the loop.
+template <int R, bool CACHED, bool HOLD>
+struct FragSet {
+  static constexpr int T = HOLD ? R / 16 : 1;
+  h8 f[T][T][2];
+  __device__ __forceinline__ void init(const h8* __restrict__ ftab, int lane) {
+    if constexpr (HOLD) {
+#pragma unroll
+      for (int a = 0; a < T; a++)
+#pragma unroll
+        for (int b = 0; b < T; b++)
+#pragma unroll
+          for (int k = 0; k < 2; k++) {
+            f[a][b][k] = cf_frag<R, CACHED>(ftab, a, b, k, lane);
+            asm volatile("" : "+v"(f[a][b][k]));
+          }
+    }
+  }
+  __device__ __forceinline__ h8 get(const h8* __restrict__ ftab, int a, int b, int kind, int lane) const {
+    if constexpr (HOLD) return f[a][b][kind];
+    else return cf_frag<R, CACHED>(ftab, a, b, kind, lane);
+  }
+};
+
 // w[v] = sc * exp(-2*pi*i * (e0 + step*v) / N), v = 0..3 (src/sffft.cu:106-113 for the
 // exponent): the base from v_sin/v_cos with the angle reduced to (-1/2, 1/2]
 // revolutions (e/N is exact), the others by a complex recurrence.
@@ -515,6 +541,19 @@ __device__ __forceinline__ void phase2_s3(_Float16* re, _Float16* im, const floa
   constexpr float sc2 = R2 == 16 ? 0.25f : R2 == 32 ? 0.17677669529663687f : 0.125f;
   const int c = lane & 15, g = lane >> 4;
   h4 outr[ROWS][T1][T2], outi[ROWS][T1][T2];  // [row][n1 tile][n2 tile]
+  // In-kernel DFT fragments (legacy plans) are evaluated once for all rows when both
+  // radices' sets fit in 40 VGPRs; table fragments are read at each use (holding them
+  // measured no faster).
+  constexpr bool HOLD = !CACHED && 8 * (T1 * T1 + (R1 == R2 ? 0 : T2 * T2)) <= 40;
+  FragSet<R1, CACHED, HOLD> F1;
+  FragSet<R2, CACHED, HOLD && R1 != R2> F2;
+  F1.init(ftab, lane);
+  F2.init(ftab, lane);
+  auto f1 = [&](int a, int b, int k) { return F1.get(ftab, a, b, k, lane); };
+  auto f2 = [&](int a, int b, int k) {
+    if constexpr (R1 == R2) return F1.get(ftab, a, b, k, lane);
+    else return F2.get(ftab, a, b, k, lane);
+  };
   // The twiddles after the stage over n1 and after the inverse over k2 do not depend on
   // the row: w^(R0 k1 n2) at (k1, n2) = (16nt + c, 16t + 4g + v) and (16t + 4g + v, 16nt + c),
   // the same values when R1 == R2. With one tile per axis they are evaluated once per
@@ -580,8 +619,8 @@ __device__ __forceinline__ void phase2_s3(_Float16* re, _Float16* im, const floa
           f4 dr = {0.f, 0.f, 0.f, 0.f}, di = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
           for (int ks = 0; ks < T1; ks++) {
-            dr = mfma(a[t2][ks], cf_frag<R1, CACHED>(ftab, nt, ks, 0, lane), dr);
-            di = mfma(a[t2][ks], cf_frag<R1, CACHED>(ftab, nt, ks, 1, lane), di);
+            dr = mfma(a[t2][ks], f1(nt, ks, 0), dr);
+            di = mfma(a[t2][ks], f1(nt, ks, 1), di);
           }
           dr = round_acc(dr, acc16);
           di = round_acc(di, acc16);
@@ -605,8 +644,8 @@ __device__ __forceinline__ void phase2_s3(_Float16* re, _Float16* im, const floa
         for (int ks = 0; ks < T2; ks++)
 #pragma unroll
           for (int p = 0; p <= SB; p++) {
-            dr[mt] = mfma(cf_frag<R2, CACHED>(ftab, mt, ks, 0, lane), b[t1][ks][p], dr[mt]);
-            di[mt] = mfma(cf_frag<R2, CACHED>(ftab, mt, ks, 1, lane), b[t1][ks][p], di[mt]);
+            dr[mt] = mfma(f2(mt, ks, 0), b[t1][ks][p], dr[mt]);
+            di[mt] = mfma(f2(mt, ks, 1), b[t1][ks][p], di[mt]);
           }
         dr[mt] = round_acc(dr[mt], acc16);
         di[mt] = round_acc(di[mt], acc16);
@@ -618,11 +657,11 @@ __device__ __forceinline__ void phase2_s3(_Float16* re, _Float16* im, const floa
         f4 er = {0.f, 0.f, 0.f, 0.f}, ei = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int mt = 0; mt < T2; mt++) {
-          er = mfma(a2[mt], cf_frag<R2, CACHED>(ftab, nt, mt, 0, lane), er);
-          ei = mfma(a2[mt], cf_frag<R2, CACHED>(ftab, nt, mt, 1, lane), ei);
+          er = mfma(a2[mt], f2(nt, mt, 0), er);
+          ei = mfma(a2[mt], f2(nt, mt, 1), ei);
           if constexpr (SA) {
-            er = mfma(a2lo[mt], cf_frag<R2, CACHED>(ftab, nt, mt, 0, lane), er);
-            ei = mfma(a2lo[mt], cf_frag<R2, CACHED>(ftab, nt, mt, 1, lane), ei);
+            er = mfma(a2lo[mt], f2(nt, mt, 0), er);
+            ei = mfma(a2lo[mt], f2(nt, mt, 1), ei);
           }
         }
         er = round_acc(er, acc16);
@@ -643,8 +682,8 @@ __device__ __forceinline__ void phase2_s3(_Float16* re, _Float16* im, const floa
         for (int ks = 0; ks < T1; ks++)
 #pragma unroll
           for (int p = 0; p <= SE; p++) {
-            zr = mfma(cf_frag<R1, CACHED>(ftab, mt, ks, 0, lane), e[nt][ks][p], zr);
-            zi = mfma(cf_frag<R1, CACHED>(ftab, mt, ks, 1, lane), e[nt][ks][p], zi);
+            zr = mfma(f1(mt, ks, 0), e[nt][ks][p], zr);
+            zi = mfma(f1(mt, ks, 1), e[nt][ks][p], zi);
           }
         zr = round_acc(zr, acc16);
         zi = round_acc(zi, acc16);
