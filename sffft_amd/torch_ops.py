@@ -13,10 +13,16 @@ long-convolution layers of Hyena/H3/S4-style models (README.md:11). This module 
 (meta) implementations, so they trace under ``torch.compile`` and ``torch.export``, and they are
 plain stream-ordered launches, so they capture into CUDA/HIP graphs.
 
-Gradients: ``conv`` is differentiable in u. Causal convolution's adjoint is the anti-causal
-correlation du[m] = sum_{n >= m} dy[n] k[n - m], which is flip(causal_conv(flip(dy), k)), so the
-backward pass runs the same kernel on the same spectrum. The filter gradient (a reduction over
-the batch) is not provided: ``spectrum`` raises if its filter requires grad.
+Gradients:
+
+- ``conv`` is differentiable in u. Causal convolution's adjoint is the anti-causal correlation
+  du[m] = sum_{n >= m} dy[n] k[n - m], which is flip(causal_conv(flip(dy), k)): the backward pass
+  runs the same kernel on the same spectrum.
+- ``LongConv`` is differentiable in u and in the filter k. The filter gradient is the
+  batch-summed correlation dk[h, j] = sum_b sum_{n >= j} dy[b, h, n] u[b, h, n - j]. Per sequence
+  this is flip(causal_conv(flip(dy), u)), with u as the filter (``filter_grad``): the B*H input
+  rows become filters of a batch-of-one convolution of the flipped output gradients.
+- ``spectrum`` itself has no gradient and raises if its filter requires grad.
 """
 from __future__ import annotations
 
@@ -98,12 +104,48 @@ def _conv_backward(ctx, dy):
 conv.register_autograd(_conv_backward, setup_context=_conv_setup)
 
 
+def filter_grad(u: torch.Tensor, dy: torch.Tensor) -> torch.Tensor:
+    """dk[h, j] = sum_b sum_{n >= j} dy[b, h, n] u[b, h, n - j] for u, dy [B, H, L] (fp32 [H, L]).
+
+    Computed on the GPU kernels as flip(causal_conv(flip(dy), u)) per sequence, summed over b:
+    the B*H rows of u are the filters (fp32 spectra) of a batch-of-one convolution.
+    """
+    B, H, L = u.shape
+    plan = default_plan(L, "fp32", 1)  # one sequence per transform: batch of one
+    fields = plan_fields(plan)
+    kf = torch.ops.sffft.spectrum(u.detach().float().reshape(B * H, L).contiguous(), fields)
+    w = dy.float().flip(-1).reshape(1, B * H, L).contiguous()
+    r = torch.ops.sffft.conv(w, kf, fields)
+    return r.reshape(B, H, L).flip(-1).sum(0)
+
+
+class _LongConvFn(torch.autograd.Function):
+    """y = conv(u, kf) with gradients for u and for the filter k that kf was made from."""
+
+    @staticmethod
+    def forward(ctx, u, k, kf, fields):
+        ctx.save_for_backward(u, kf)
+        ctx.fields = list(fields)
+        return torch.ops.sffft.conv(u, kf, fields)
+
+    @staticmethod
+    def backward(ctx, dy):
+        u, kf = ctx.saved_tensors
+        du = dk = None
+        if ctx.needs_input_grad[0]:
+            du = torch.ops.sffft.conv(dy.flip(-1).contiguous().to(u.dtype), kf, ctx.fields).flip(-1)
+        if ctx.needs_input_grad[1]:
+            dk = filter_grad(u, dy)
+        return du, dk, None, None
+
+
 class LongConv:
     """Causal long convolution y = causal_conv(u, k) with the filter spectrum cached.
 
     The spectrum of a filter tensor is kept while the tensor lives and is recomputed when it is
-    modified in place (its version counter moves) or when L or the plan changes. With no plan
-    given, the tuned plan for (L, dtype, B) is used.
+    modified in place (its version counter moves, as an optimizer step does) or when L or the
+    plan changes. With no plan given, the tuned plan for (L, dtype, B) is used. Differentiable in
+    u and, when it requires grad, in k (``filter_grad``).
     """
 
     def __init__(self, plan: Optional[Plan] = None):
@@ -127,7 +169,7 @@ class LongConv:
         same = hit is not None and hit[0]() is k
         if same and hit[1] == key:
             return hit[2]
-        kf = torch.ops.sffft.spectrum(k, fields)
+        kf = torch.ops.sffft.spectrum(k.detach(), fields)
         if not same:
             weakref.finalize(k, self._cache.pop, id(k), None)
         self._cache[id(k)] = (weakref.ref(k), key, kf)
@@ -136,4 +178,8 @@ class LongConv:
 
     def __call__(self, u: torch.Tensor, k: torch.Tensor) -> torch.Tensor:
         plan = self.plan_for(u)
-        return torch.ops.sffft.conv(u, self.spectrum(k, plan), plan_fields(plan))
+        fields = plan_fields(plan)
+        kf = self.spectrum(k, plan)
+        if k.requires_grad and torch.is_grad_enabled():
+            return _LongConvFn.apply(u, k, kf, fields)
+        return torch.ops.sffft.conv(u, kf, fields)

@@ -58,6 +58,29 @@ def test_adjoint_is_flipped_causal_convolution():
     assert np.abs(wrong - du).max() > 1e-3 * np.abs(du).max()
 
 
+def test_filter_gradient_is_flipped_causal_convolution():
+    """dk[h,j] = sum_b sum_{n>=j} dy[b,h,n] u[b,h,n-j] equals flip(causal_conv(flip(dy), u))
+    summed over b, with u as a per-sequence filter: the identity filter_grad runs on."""
+    rng = np.random.default_rng(5)
+    B, H, L = 3, 2, 48
+    dy = rng.standard_normal((B, H, L)).astype(np.float32)
+    u = rng.standard_normal((B, H, L)).astype(np.float32)
+    dk = np.zeros((H, L))
+    for j in range(L):
+        for n in range(j, L):
+            dk[:, j] += (dy[:, :, n].astype(np.float64) * u[:, :, n - j]).sum(0)
+    # one channel per (b, h) sequence, batch of one
+    r = oracle.direct_conv(dy[:, :, ::-1].reshape(1, B * H, L).copy(), u.reshape(B * H, L))
+    got = r.reshape(B, H, L)[:, :, ::-1].sum(0)
+    assert np.abs(got - dk).max() < 1e-9 * np.abs(dk).max()
+    # plausible mistakes (no output flip; u and dy exchanged) fail the same check
+    wrong = r.reshape(B, H, L).sum(0)
+    assert np.abs(wrong - dk).max() > 1e-3 * np.abs(dk).max()
+    r2 = oracle.direct_conv(u[:, :, ::-1].reshape(1, B * H, L).copy(), dy.reshape(B * H, L))
+    wrong2 = r2.reshape(B, H, L)[:, :, ::-1].sum(0)
+    assert np.abs(wrong2 - dk).max() > 1e-3 * np.abs(dk).max()
+
+
 # ---- GPU ----------------------------------------------------------------------------------
 
 def _inputs(dev, B, H, L, seed):
@@ -106,12 +129,52 @@ def test_input_gradient(dev, L):
 
 
 @pytest.mark.gpu
-def test_no_filter_gradient(dev):
-    u, k, _, _ = _inputs(dev, 2, 3, 256, seed=4)
+@pytest.mark.parametrize("L,io", [(512, "fp32"), (4096, "fp32"), (1024, "bf16")])
+def test_filter_gradient(dev, L, io):
+    B, H = 4, 5
+    u, k, u_np, k_np = _inputs(dev, B, H, L, seed=13)
+    if io == "bf16":
+        u = u.to(torch.bfloat16)
+        u_np = u.float().cpu().numpy()
+    w = torch.randn(B, H, L, device=dev, generator=torch.Generator(device=dev).manual_seed(3))
     k.requires_grad_()
-    y = torch_ops.LongConv()(u, k)
+    u.requires_grad_()
+    lc = torch_ops.LongConv()
+    (lc(u, k).float() * w).sum().backward()
+    # dk[h,j] = sum_b sum_{n>=j} w[b,h,n] u[b,h,n-j] in fp64 (the identity is pinned on the CPU)
+    w_np = w.cpu().numpy()
+    r = oracle.conv(w_np[:, :, ::-1].reshape(1, B * H, L).copy(), u_np.reshape(B * H, L))
+    ref = r.reshape(B, H, L)[:, :, ::-1].sum(0)
+    err = oracle.rel_l2(k.grad.cpu().numpy(), ref)
+    print(f"L={L} {io} filter-gradient rel_l2={err:.3e}", flush=True)
+    assert err <= (6e-4 if io == "fp32" else 3e-3)
+    assert u.grad is not None and u.grad.dtype == u.dtype
+
+
+@pytest.mark.gpu
+def test_spectrum_op_has_no_gradient(dev):
+    _, k, _, _ = _inputs(dev, 2, 3, 256, seed=4)
+    k.requires_grad_()
+    p = torch_ops.plan_fields(sf.default_plan(256, "fp32", 2))
+    kf = torch.ops.sffft.spectrum(k, p)
     with pytest.raises(RuntimeError, match="no gradient"):
-        y.sum().backward()
+        torch.view_as_real(kf).sum().backward()
+
+
+@pytest.mark.gpu
+def test_filter_training_step_refreshes_spectrum(dev):
+    u, k, _, _ = _inputs(dev, 2, 3, 1024, seed=8)
+    k.requires_grad_()
+    lc = torch_ops.LongConv()
+    opt = torch.optim.SGD([k], lr=0.1)
+    y0 = lc(u, k)
+    y0.square().sum().backward()
+    opt.step()
+    assert lc.spectra_computed == 1
+    y1 = lc(u, k)  # the optimizer changed k in place: a new spectrum
+    assert lc.spectra_computed == 2 and not torch.equal(y0, y1)
+    y2 = lc(u, k)
+    assert lc.spectra_computed == 2 and torch.equal(y1, y2)
 
 
 @pytest.mark.gpu
