@@ -104,8 +104,9 @@ def copy_reference(a):
 def main():
     a = parse()
     if a.gpus != 1:
-        print(f"bench.py: this build measures one GPU only (got --gpus {a.gpus}); sequences shard "
-              "trivially across GPUs by channel, see the design notes. Run with --gpus 1.", file=sys.stderr)
+        print(f"bench.py: this build measures one GPU only (got --gpus {a.gpus}); the convolution "
+              "shards across GPUs by channel with no communication (each GPU takes H/N channels "
+              "and their filters). Run with --gpus 1.", file=sys.stderr)
         sys.exit(2)
     if a.copy_mb > 0:
         copy_reference(a)
