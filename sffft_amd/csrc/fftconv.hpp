@@ -24,15 +24,20 @@
 //    slots 4..7 the imaginary parts, so Dr = [Xr|Xi].[Fr;-Fi] and
 //    Di = [Xr|Xi].[Fi;Fr] are two MFMAs per 16-wide complex K step.
 //  * The MFMA D layout (lane (c,g) holds rows 4g..4g+3 of column c) equals the
-//    A/B operand layout of the next contraction over those rows, so the last
-//    forward stage, the spectrum product and the first inverse stage run in
-//    registers without touching LDS.
-//  * Between stages the LDS layout changes so the next contraction digit is the
-//    fastest one: operand reads and accumulator writes are 8-byte vectors.
+//    A/B operand layout of the next contraction over those rows, so chained
+//    contractions stay in registers: in two-stage plans the last forward stage,
+//    the spectrum product and the first inverse stage; in three-stage plans all
+//    four stages of a k0 row (phase 2), whose input alone comes from LDS.
+//  * Between phases the LDS layout changes so the next contraction digit is the
+//    fastest one: operand reads and accumulator writes are 8-byte vectors, and
+//    XOR swizzles keep the remaining scalar writes off shared banks.
 //  * Inverse stages reuse the forward DFT fragments: IDFT(X) = conj(DFT(conj X));
 //    the conjugations are folded into the twiddle and spectrum products.
 //  * Twiddles are computed in registers with v_sin_f32/v_cos_f32 (argument in
-//    revolutions, so e/N is exact) and a 3-step complex recurrence.
+//    revolutions, so e/N is exact) and a 3-step complex recurrence; with eight
+//    rows per wavefront, the last twiddles of phase 2 step from row to row.
+//  * fp32 I/O: the input enters the first stage as an fp16 value plus its fp16
+//    remainder (SFFFT_FP32_SPLITS), removing the largest rounding term.
 #pragma once
 #include <hip/hip_runtime.h>
 #include <stdint.h>
