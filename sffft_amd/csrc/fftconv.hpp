@@ -82,8 +82,7 @@ struct Plan {
   static constexpr int M = N / R0;           // positions per first-digit row
   static constexpr int PA = R1 + LDS_PAD;    // pitch: rows whose fastest digit is n1/k1
   static constexpr int PB = R0 + LDS_PAD;    // pitch: [m][k0], input of the last inverse stage
-  static constexpr int PC = R2 + LDS_PAD;    // pitch: [k1][n2] (three-stage only)
-  static constexpr int ROW = S == 3 ? cmax(R2 * PA, R1 * PC) : 0;
+  static constexpr int ROW = S == 3 ? R2 * PA : 0;  // one k0 row of [k0][n2][n1] (three-stage)
   static constexpr int PLANE0 = S == 3 ? cmax(R0 * ROW, M * PB) : cmax(R0 * PA, R1 * PB);
   static constexpr int PLANE = (PLANE0 + 63) & ~63;
   static constexpr int LDS_BYTES = 2 * PLANE * 2;
@@ -251,14 +250,6 @@ __device__ __forceinline__ h8 lds_frag(const _Float16* re, const _Float16* im, i
 }
 __device__ __forceinline__ h4 to_h4(const float* x) {
   return (h4){(_Float16)x[0], (_Float16)x[1], (_Float16)x[2], (_Float16)x[3]};
-}
-
-__device__ __forceinline__ void wave_sync() {
-  // LDS operations of one wavefront execute in order; this keeps the compiler
-  // from moving LDS accesses across the point where lanes exchange data.
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
 // ---- Phase 1: first forward stage over n0 (src/sffft.cu:266-274) ---------------
