@@ -561,17 +561,19 @@ __device__ __forceinline__ void phase2_s3(_Float16* re, _Float16* im, const floa
   };
   // The twiddles after the stage over n1 and after the inverse over k2 do not depend on
   // the row: w^(R0 k1 n2) at (k1, n2) = (16nt + c, 16t + 4g + v) and (16t + 4g + v, 16nt + c),
-  // the same values when R1 == R2. With one tile per axis they are evaluated once per
-  // wavefront instead of twice per row.
+  // the same values when R1 == R2. With one tile per axis (R1 = R2 = 16) they are
+  // evaluated once per wavefront, with their common scale 1/sqrt(16), instead of twice
+  // per row.
   constexpr bool SHARED_TW = T1 == 1 && T2 == 1;
+  static_assert(!SHARED_TW || sc1 == sc2, "one tile per axis: equal radices");
   float twr[4], twi[4];
-  if constexpr (SHARED_TW) twiddle4<N>(R0 * c, 4 * g, 1.f, twr, twi);
+  if constexpr (SHARED_TW) twiddle4<N>(R0 * c, 4 * g, sc1, twr, twi);
   auto tw_n1 = [&](int nt, int t2, float sc, float* wr, float* wi) {
     if constexpr (SHARED_TW) {
 #pragma unroll
       for (int v = 0; v < 4; v++) {
-        wr[v] = sc * twr[v];
-        wi[v] = sc * twi[v];
+        wr[v] = twr[v];
+        wi[v] = twi[v];
       }
     } else {
       twiddle4<N>(R0 * (16 * nt + c), 16 * t2 + 4 * g, sc, wr, wi);
