@@ -154,8 +154,8 @@ DEFAULT_PLANS = {
     (1024, "fp32"): ("64x32", 12, 2, 1, 3), (1024, "bf16"): ("64x32", 12, 2, 1, 3),
     (2048, "fp32"): ("64x64", 12, 2, 1, 3), (2048, "bf16"): ("64x64", 12, 2, 1, 3),
     (4096, "fp32"): ("32x16x16", 8, 2, 0, 1), (4096, "bf16"): ("32x16x16", 8, 2, 0, 1),
-    (8192, "fp32"): ("64x16x16", 8, 2, 0, 1), (8192, "bf16"): ("64x16x16", 8, 2, 0, 1),
-    (16384, "fp32"): ("32x32x32", 8, 2, 0, 1), (16384, "bf16"): ("32x32x32", 8, 2, 0, 1),
+    (8192, "fp32"): ("32x32x16", 8, 2, 0, 1), (8192, "bf16"): ("64x16x16", 8, 2, 0, 1),
+    (16384, "fp32"): ("32x32x32", 16, 2, 0, 1), (16384, "bf16"): ("32x32x32", 16, 2, 0, 1),
 }
 # One sequence per transform (workgroup kernel) for an odd batch
 ODD_BATCH_PLANS = {128: ("16x16", 2), 256: ("32x16", 2), 512: ("32x32", 2), 1024: ("64x32", 4),

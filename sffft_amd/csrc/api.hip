@@ -51,7 +51,7 @@ size_t lds_bytes_rt(int r0, int r1, int r2, int mode, int channels, int waves) {
   const int S = r2 > 1 ? 3 : 2, N = r0 * r1 * r2, M = N / r0;
   const int PA = r1 + LDS_PAD, PB = r0 + LDS_PAD;
   const int ROW = S == 3 ? r2 * PA : 0;
-  const int P0 = S == 3 ? cmax(r0 * ROW, M * PB) : cmax(r0 * PA, r1 * PB);
+  const int P0 = S == 3 ? r0 * ROW : cmax(r0 * PA, r1 * PB);
   return (size_t)(((P0 + 63) & ~63) * 4);
 }
 

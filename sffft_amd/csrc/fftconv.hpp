@@ -81,17 +81,11 @@ struct Plan {
   static constexpr int N = R0 * R1 * R2, L = N / 2;
   static constexpr int M = N / R0;           // positions per first-digit row
   static constexpr int PA = R1 + LDS_PAD;    // pitch: rows whose fastest digit is n1/k1
-  static constexpr int PB = R0 + LDS_PAD;    // pitch: [m][k0], input of the last inverse stage
+  static constexpr int PB = R0 + LDS_PAD;    // pitch: [m][k0], input of the last inverse stage (two-stage)
   static constexpr int ROW = S == 3 ? R2 * PA : 0;  // one k0 row of [k0][n2][n1] (three-stage)
-  static constexpr int PLANE0 = S == 3 ? cmax(R0 * ROW, M * PB) : cmax(R0 * PA, R1 * PB);
+  static constexpr int PLANE0 = S == 3 ? R0 * ROW : cmax(R0 * PA, R1 * PB);
   static constexpr int PLANE = (PLANE0 + 63) & ~63;
   static constexpr int LDS_BYTES = 2 * PLANE * 2;
-  // Column of k0 group c4 (a multiple of 4) in row block mt of the [m][k0] plane:
-  // three-stage plans write it swizzled with the 16-row block's index m / R2 (phase2_s3).
-  __device__ static int s3_col(int mt, int c4) {
-    if constexpr (S == 3) return c4 ^ (4 * (((16 * mt) / R2) & (R0 / 4 - 1)));
-    else return c4;
-  }
   static_assert(R0 >= 16 && R1 >= 16 && (S == 2 || R2 >= 16), "radices are 16, 32 or 64");
   static_assert(R0 <= 64 && R1 <= 64 && R2 <= 64, "radices are 16, 32 or 64");
 };
@@ -545,7 +539,6 @@ __device__ __forceinline__ void phase2_s3(_Float16* re, _Float16* im, const floa
   constexpr float sc1 = R1 == 16 ? 0.25f : R1 == 32 ? 0.17677669529663687f : 0.125f;
   constexpr float sc2 = R2 == 16 ? 0.25f : R2 == 32 ? 0.17677669529663687f : 0.125f;
   const int c = lane & 15, g = lane >> 4;
-  h4 outr[ROWS][T1][T2], outi[ROWS][T1][T2];  // [row][n1 tile][n2 tile]
   // In-kernel DFT fragments (legacy plans) are evaluated once for all rows when both
   // radices' sets fit in 40 VGPRs; table fragments are read at each use (holding them
   // measured no faster).
@@ -613,9 +606,7 @@ __device__ __forceinline__ void phase2_s3(_Float16* re, _Float16* im, const floa
   }
 #pragma unroll
   for (int i = 0; i < ROWS; i++) {
-    // each wavefront owns ROWS consecutive rows, so the final [m][k0] write stores
-    // consecutive k0 of one m as one vector
-    const int k0 = wave * ROWS + i;
+    const int k0 = wave * ROWS + i;  // each wavefront owns ROWS consecutive rows
     const int rb = k0 * P::ROW;
     if constexpr (KQB == 2) {
       if (i + 1 < ROWS) load_row_spectrum(k0 + 1, kq[(i + 1) & 1]);
@@ -716,52 +707,14 @@ __device__ __forceinline__ void phase2_s3(_Float16* re, _Float16* im, const floa
           twiddle4e<N>(k0 * ((16 * mt + 4 * g) * R2 + 16 * nt + c), k0 * R2, sc1, wr, wi);
         }
         twiddle(zr, zi, wr, wi, xr, xi);
-        outr[i][mt][nt] = to_h4(xr);
-        outi[i][mt][nt] = to_h4(xi);
-        // With one tile per axis, computed here rather than sunk to the final write,
-        // which would keep every row's accumulators and twiddle live to the end
-        // (measured: faster with one tile per axis, slower with more).
-        if constexpr (T1 * T2 == 1) asm volatile("" : "+v"(outr[i][mt][nt]), "+v"(outi[i][mt][nt]));
+        // back into the row's own block, [n2][n1]: only this wavefront reads the row,
+        // and all of its input is in registers by now
+        const int pos = rb + (16 * nt + c) * P::PA + 16 * mt + 4 * g;
+        *reinterpret_cast<h4*>(re + pos) = to_h4(xr);
+        *reinterpret_cast<h4*>(im + pos) = to_h4(xi);
       }
     }
   }
-  __syncthreads();  // every row has been read before the [m][k0] layout is written
-  // [m][k0]: the wavefront's ROWS consecutive k0 of one m are written as one vector
-  // (up to 4 halves). The k0 column is swizzled in groups of 4 with the row's n1 =
-  // m / R2, k0 ^ 4*(n1 mod R0/4), which phase3 undoes (P::s3_col): rows R2 apart (a
-  // multiple of the bank count) then fall on different banks.
-  constexpr int G = ROWS < 4 ? ROWS : 4;
-#pragma unroll
-  for (int mt = 0; mt < T1; mt++)
-#pragma unroll
-    for (int nt = 0; nt < T2; nt++)
-#pragma unroll
-      for (int v = 0; v < 4; v++) {
-        const int n1 = 16 * mt + 4 * g + v, m = n1 * R2 + 16 * nt + c;
-#pragma unroll
-        for (int q = 0; q < ROWS / G; q++) {
-          const int col = (wave * ROWS + q * G) ^ (4 * (n1 & (R0 / 4 - 1)));
-          _Float16 hr[G], hi[G];
-#pragma unroll
-          for (int j = 0; j < G; j++) {
-            hr[j] = outr[q * G + j][mt][nt][v];
-            hi[j] = outi[q * G + j][mt][nt][v];
-          }
-          _Float16* pr = re + m * P::PB + col;
-          _Float16* pi = im + m * P::PB + col;
-          if constexpr (G == 4) {
-            *reinterpret_cast<h4*>(pr) = (h4){hr[0], hr[1], hr[2], hr[3]};
-            *reinterpret_cast<h4*>(pi) = (h4){hi[0], hi[1], hi[2], hi[3]};
-          } else if constexpr (G == 2) {
-            typedef _Float16 h2 __attribute__((ext_vector_type(2)));
-            *reinterpret_cast<h2*>(pr) = (h2){hr[0], hr[1]};
-            *reinterpret_cast<h2*>(pi) = (h2){hi[0], hi[1]};
-          } else {
-            *pr = hr[0];
-            *pi = hi[0];
-          }
-        }
-      }
 }
 
 // ---- Phase 3: last inverse stage over k0, first L outputs only -----------------
@@ -799,8 +752,23 @@ __device__ __forceinline__ void phase3(TIO* __restrict__ ya, TIO* __restrict__ y
     }
   };
   auto load = [&](int mt, h8* a) {
+    if constexpr (P::S == 3) {
+      // A[m][k0] from the rows [k0][n2][n1] that phase 2 wrote: four k0 per lane, one
+      // row apart, read as 16-bit elements
+      constexpr int R2 = P::R2;
+      const int m = 16 * mt + r, base = (m % R2) * P::PA + m / R2;
 #pragma unroll
-    for (int ks = 0; ks < KS; ks++) a[ks] = lds_frag(re, im, (16 * mt + r) * P::PB + P::s3_col(mt, 16 * ks + 4 * g));
+      for (int ks = 0; ks < KS; ks++)
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+          const int at = (16 * ks + 4 * g + j) * P::ROW + base;
+          a[ks][j] = re[at];
+          a[ks][4 + j] = im[at];
+        }
+    } else {
+#pragma unroll
+      for (int ks = 0; ks < KS; ks++) a[ks] = lds_frag(re, im, (16 * mt + r) * P::PB + 16 * ks + 4 * g);
+    }
   };
   if constexpr (MT >= NW) {
     for (int mt = wave; mt < MT; mt += NW) {
