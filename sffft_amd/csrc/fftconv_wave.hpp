@@ -26,7 +26,8 @@
 //
 // Read-only tables in LDS, filled once per workgroup:
 //   F0, F1 : DFT fragments of radix R0 and R1, both kinds ([cos | sin] and
-//            [-sin | cos]) in the order of the coefficient table
+//            [-sin | cos]) in the order of the coefficient table (the first kind
+//            only in the strided layout, see WavePlan)
 //   TW1    : sc0 * w^(m k0) in the lane order of the phase-1 result tiles
 //   TW2    : sc1 * sc0 * w^(k0 n1) in the lane order of the inverse result tiles
 // so no twiddle is evaluated in the loop and no per-stage scale is applied; the
@@ -41,6 +42,8 @@
 
 namespace sffft {
 
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
 template <int R0_, int R1_>
 struct WavePlan {
   static constexpr int R0 = R0_, R1 = R1_, N = R0 * R1, L = N / 2, M = R1;
@@ -54,20 +57,30 @@ struct WavePlan {
   static constexpr int SP_F4 = N / 2;  // one channel's spectrum: N complex64 = N/2 float4
   static constexpr int TW_TABLES = R0 == R1 ? 1 : 2;
   static constexpr int TAB_F4 = F0_H8 + F1_H8 + TW_TABLES * TW_F4;
+  // the same with the first fragment kind only (the second is derived in registers)
+  static constexpr int TAB1_F4 = (F0_H8 + F1_H8) / 2 + TW_TABLES * TW_F4;
   // per-wavefront operand scratch of the row loads with fp32 I/O (bf16 needs less)
   static constexpr int SCRATCH_MAX = 16 * (M + 4) * 4;
+  // per-wavefront output scratch of one store round (1 KB of whole rows) for an I/O
+  // element of `es` bytes, at the pitch of the row scratch
+  static constexpr int out_rows(int es) { return 64 * (16 / es) / M < 16 ? 64 * (16 / es) / M : 16; }
+  static constexpr int out_scratch(int es) { return out_rows(es) * (M + (es == 4 ? 4 : 8)) * es; }
+  static constexpr int OUT_SCRATCH_MAX = out_scratch(4) > out_scratch(2) ? out_scratch(4) : out_scratch(2);
   // Layout choice for a workgroup of nw wavefronts serving ch channels, in order of
-  // preference: row loads and spectra in LDS; strided loads (no scratch) and spectra
-  // in LDS; row loads and spectra read from global memory.
+  // preference: row loads and spectra in LDS; strided loads, spectra in LDS, the
+  // first fragment kind only and an output scratch of one store round; row loads
+  // and spectra read from global memory.
   static constexpr int tables_and_spectra_bytes(int ch) { return (TAB_F4 + ch * SP_F4) * 16; }
   static constexpr bool row_loads(int ch, int nw) {
     return tables_and_spectra_bytes(ch) + nw * SCRATCH_MAX <= 163840 || tables_and_spectra_bytes(ch) > 163840;
   }
+  static constexpr int tables_f4(int ch, int nw) { return row_loads(ch, nw) ? TAB_F4 : TAB1_F4; }
+  static constexpr int scratch_max(int ch, int nw) { return row_loads(ch, nw) ? SCRATCH_MAX : OUT_SCRATCH_MAX; }
   static constexpr bool spectra_in_lds(int ch, int nw) {
-    return tables_and_spectra_bytes(ch) + (row_loads(ch, nw) ? nw * SCRATCH_MAX : 0) <= 163840;
+    return (tables_f4(ch, nw) + ch * SP_F4) * 16 + nw * scratch_max(ch, nw) <= 163840;
   }
   static constexpr int lds_bytes(int ch, int nw) {
-    return (TAB_F4 + (spectra_in_lds(ch, nw) ? ch * SP_F4 : 0)) * 16 + (row_loads(ch, nw) ? nw * SCRATCH_MAX : 0);
+    return (tables_f4(ch, nw) + (spectra_in_lds(ch, nw) ? ch * SP_F4 : 0)) * 16 + nw * scratch_max(ch, nw);
   }
   static_assert(R0 >= 16 && R0 <= 64 && R1 >= 16 && R1 <= 64, "radices are 16, 32 or 64");
 };
@@ -78,10 +91,21 @@ __host__ __device__ constexpr int tw_index(int tile, int lane, int q) { return (
 // q as above; lanes at 16-byte stride so one load instruction reads 1 KB.
 __host__ __device__ constexpr int sp_index(int tile, int lane, int q) { return (tile * 2 + q) * 64 + lane; }
 
-// DFT fragment (a, b, kind) of a radix-R table in LDS (coefficient-table order).
-template <int R>
+// DFT fragment (a, b, kind) of a radix-R table in LDS: coefficient-table order, or
+// with K1 the first kind [cos | sin] only. The second kind [-sin | cos] is then the
+// first with its halves swapped and the new first half negated: read with the halves
+// exchanged, then two sign flips. This is exact, as the table rounds -sin to the
+// negation of the rounded sin.
+template <int R, bool K1 = false>
 __device__ __forceinline__ h8 dft_frag(const h8* F, int a, int b, int kind, int lane) {
-  return F[((a * (R / 16) + b) * 2 + kind) * 64 + lane];
+  if constexpr (K1) {
+    const u32x2* p = reinterpret_cast<const u32x2*>(F + (a * (R / 16) + b) * 64 + lane);
+    const u32x2 c = p[0], s = p[1];
+    if (kind == 0) return __builtin_bit_cast(h8, (u32x4){c.x, c.y, s.x, s.y});
+    return __builtin_bit_cast(h8, (u32x4){s.x ^ 0x80008000u, s.y ^ 0x80008000u, c.x, c.y});
+  } else {
+    return F[((a * (R / 16) + b) * 2 + kind) * 64 + lane];
+  }
 }
 
 // (dr + i di) * w for four values, packed as an operand fragment [re | im] in fp16.
@@ -121,10 +145,6 @@ __device__ __forceinline__ f4 acc_round(f4 v) {
 
 __device__ __forceinline__ float4 ld_f4(const float4* p) { return *p; }
 
-// Per-lane output pieces (plans without the operand scratch): plain write-back
-// stores, so L2 merges the partial lines before they reach HBM.
-__device__ __forceinline__ void store4(float* p, f4 v) { *reinterpret_cast<f4*>(p) = v; }
-__device__ __forceinline__ void store4(uint16_t* p, f4 v) { *reinterpret_cast<u32x2*>(p) = f4_to_bf16x4(v); }
 
 // 16-byte blocks copied from global memory straight into LDS (global_load_lds_dwordx4:
 // lane i of the wave writes bytes [16i, 16i+16) after the wave-uniform LDS base).
@@ -159,16 +179,16 @@ __device__ __forceinline__ void wait_vmcnt() {
   __builtin_amdgcn_s_waitcnt((V & 15) | ((V >> 4) << 14) | (7 << 4) | (15 << 8));
 }
 
-// DFT fragments of radix R (both kinds) computed into LDS (the in-kernel "legacy"
-// source), in coefficient-table order.
-template <int R, int NTH>
+// DFT fragments of radix R (both kinds, or with K1 the first only) computed into LDS
+// (the in-kernel "legacy" source), in coefficient-table order.
+template <int R, int NTH, bool K1 = false>
 __device__ __forceinline__ void compute_dft(h8* dst, int tid) {
-  constexpr int T = R / 16, TOTAL = T * T * 128;
+  constexpr int T = R / 16, KINDS = K1 ? 1 : 2, TOTAL = T * T * 64 * KINDS;
 #pragma unroll
   for (int i = 0; i < (TOTAL + NTH - 1) / NTH; i++) {
     const int k = tid + i * NTH;
     if (TOTAL % NTH == 0 || k < TOTAL) {
-      const int ab = k >> 7, kind = (k >> 6) & 1;
+      const int ab = k / (64 * KINDS), kind = K1 ? 0 : (k >> 6) & 1;
       dst[k] = cf_frag<R, false>(nullptr, ab / T, ab % T, kind, k & 63);
     }
   }
@@ -178,7 +198,6 @@ __device__ __forceinline__ void compute_dft(h8* dst, int tid) {
 // its length-2L transform input and are contiguous, so both rows are read as 16-byte
 // chunks, one KB per instruction, with the streaming (non-temporal) hint: chunk q of
 // the pair (rows a then b) goes to lane q % 64 of round q / 64.
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 template <class P, class TIO, bool ROWS>
 struct PairLoads;
@@ -347,6 +366,32 @@ __device__ __forceinline__ void store_rows(TIO* S, const f4 (&z)[P::MT], TIO* __
   __asm__ volatile("" ::: "memory");
 }
 
+// The same through a scratch of one store round only (the strided layout): the
+// 16-row block goes out in rounds of P::out_rows rows (1 KB, whole rows), each staged
+// by the 16 lanes that hold those rows.
+template <class P, class TIO>
+__device__ __forceinline__ void store_rounds(TIO* S, const f4 (&z)[P::MT], TIO* __restrict__ y, int lane) {
+  constexpr int M = P::M, PITCH = scratch_pitch<P, TIO>(), EPC = 16 / (int)sizeof(TIO), CPR = M / EPC;
+  constexpr int RPR = P::out_rows((int)sizeof(TIO));
+  static_assert(P::R0 >= 32 && 16 % RPR == 0 && RPR * CPR <= 64, "16 stored rows in whole rounds");
+  const int c = lane & 15, g = lane >> 4;
+#pragma unroll
+  for (int q = 0; q < 16 / RPR; q++) {
+    if (c / RPR == q) {
+#pragma unroll
+      for (int t = 0; t < P::MT; t++) put4(S + (c % RPR) * PITCH + 16 * t + 4 * g, z[t]);
+    }
+    // other lanes' writes are read below, and the next round's writes follow these
+    // reads (see pair_operands)
+    __asm__ volatile("" ::: "memory");
+    const int row = lane / CPR, col = (lane % CPR) * EPC;
+    if (RPR * CPR == 64 || row < RPR)
+      __builtin_nontemporal_store(*reinterpret_cast<const u32x4*>(S + row * PITCH + col),
+                                  reinterpret_cast<u32x4*>(y + (q * RPR + row) * M + col));
+    __asm__ volatile("" ::: "memory");
+  }
+}
+
 // Every stage of one pair, from its loaded operands to the stored outputs; SP is the
 // channel's spectrum in LDS.
 template <class P, class TIO, bool ACC16, bool HOLD_F1, bool ROWS>
@@ -354,7 +399,7 @@ __device__ __forceinline__ void process_pair(const PairLoads<P, TIO, ROWS>& d, T
                                              TIO* __restrict__ ya, TIO* __restrict__ yb, const h8* F0,
                                              const h8* F1, const float4* TW1, const float4* TW2, int lane) {
   constexpr int R0 = P::R0, M = P::M, MT = P::MT, ST = P::ST, KS1 = P::KS1, NT3 = P::NT3;
-  const int r = lane & 15, g = lane >> 4;
+  constexpr bool K1 = !ROWS;  // the strided layout keeps the first fragment kind only
   // With 16 tiles per transform (64x64) the pair alone fills 64 VGPRs; compiler-only
   // barriers at the top of each tile step keep the next step's table and spectrum
   // loads from being hoisted over the current one, which would not fit beside it.
@@ -373,8 +418,8 @@ __device__ __forceinline__ void process_pair(const PairLoads<P, TIO, ROWS>& d, T
     h8 f0[KS1], f1[KS1];
 #pragma unroll
     for (int ks = 0; ks < KS1; ks++) {
-      f0[ks] = dft_frag<R0>(F0, nt, ks, 0, lane);
-      f1[ks] = dft_frag<R0>(F0, nt, ks, 1, lane);
+      f0[ks] = dft_frag<R0, K1>(F0, nt, ks, 0, lane);
+      f1[ks] = dft_frag<R0, K1>(F0, nt, ks, 1, lane);
     }
 #pragma unroll
     for (int mt = 0; mt < MT; mt++) {
@@ -399,11 +444,11 @@ __device__ __forceinline__ void process_pair(const PairLoads<P, TIO, ROWS>& d, T
 #pragma unroll
       for (int k = 0; k < MT; k++)
 #pragma unroll
-        for (int kind = 0; kind < 2; kind++) g0[i][k][kind] = dft_frag<P::R1>(F1, i, k, kind, lane);
+        for (int kind = 0; kind < 2; kind++) g0[i][k][kind] = dft_frag<P::R1, K1>(F1, i, k, kind, lane);
   }
   auto f1frag = [&](int i, int k, int kind) -> h8 {
     if constexpr (HOLD_F1) return g0[i][k][kind];
-    else return dft_frag<P::R1>(F1, i, k, kind, lane);
+    else return dft_frag<P::R1, K1>(F1, i, k, kind, lane);
   };
 #pragma unroll
   for (int s = 0; s < ST; s++) {
@@ -442,35 +487,43 @@ __device__ __forceinline__ void process_pair(const PairLoads<P, TIO, ROWS>& d, T
 #pragma unroll
   for (int nu = 0; nu < NT3; nu++) {
     step_fence();
-    h8 f0[ST], f1[ST];
-#pragma unroll
-    for (int s = 0; s < ST; s++) {
-      f0[s] = dft_frag<R0>(F0, nu, s, 0, lane);
-      f1[s] = dft_frag<R0>(F0, nu, s, 1, lane);
-    }
-    const int n0 = 16 * nu + r;
-    f4 za[MT] = {}, zb[MT] = {};
-#pragma unroll
-    for (int t = 0; t < MT; t++) {
+    if constexpr (ROWS) {
+      h8 f0[ST], f1[ST];
 #pragma unroll
       for (int s = 0; s < ST; s++) {
-        za[t] = mfma(b2[t][s], f0[s], za[t]);
-        zb[t] = mfma(b2[t][s], f1[s], zb[t]);
+        f0[s] = dft_frag<R0, K1>(F0, nu, s, 0, lane);
+        f1[s] = dft_frag<R0, K1>(F0, nu, s, 1, lane);
       }
-      za[t] = acc_round<ACC16>(za[t]);
-      zb[t] = -acc_round<ACC16>(zb[t]);  // row b is minus the imaginary part
-      if constexpr (!ROWS) {
-        // no scratch: each lane stores its own 16-byte (fp32) or 8-byte (bf16) piece
-        if (R0 >= 32 || n0 < R0 / 2) {
-          const int o = n0 * M + 16 * t + 4 * g;
-          store4(ya + o, za[t]);
-          store4(yb + o, zb[t]);
+      f4 za[MT] = {}, zb[MT] = {};
+#pragma unroll
+      for (int t = 0; t < MT; t++) {
+#pragma unroll
+        for (int s = 0; s < ST; s++) {
+          za[t] = mfma(b2[t][s], f0[s], za[t]);
+          zb[t] = mfma(b2[t][s], f1[s], zb[t]);
         }
+        za[t] = acc_round<ACC16>(za[t]);
+        zb[t] = -acc_round<ACC16>(zb[t]);  // row b is minus the imaginary part
       }
-    }
-    if constexpr (ROWS) {
       store_rows<P, TIO>(S, za, ya + 16 * nu * M, lane);
       store_rows<P, TIO>(S, zb, yb + 16 * nu * M, lane);
+    } else {
+      // one row at a time: its 16-row block stays live through the store rounds, so
+      // the other row's fragments and results are not made before it is stored
+#pragma unroll
+      for (int kind = 0; kind < 2; kind++) {
+        h8 f[ST];
+#pragma unroll
+        for (int s = 0; s < ST; s++) f[s] = dft_frag<R0, K1>(F0, nu, s, kind, lane);
+        f4 z[MT] = {};
+#pragma unroll
+        for (int t = 0; t < MT; t++) {
+#pragma unroll
+          for (int s = 0; s < ST; s++) z[t] = mfma(b2[t][s], f[s], z[t]);
+          z[t] = kind == 0 ? acc_round<ACC16>(z[t]) : -acc_round<ACC16>(z[t]);
+        }
+        store_rounds<P, TIO>(S, z, (kind == 0 ? ya : yb) + 16 * nu * M, lane);
+      }
     }
   }
 }
@@ -485,34 +538,36 @@ __global__ void __launch_bounds__(64 * NW)
     fftconv_wave_kernel(const TIO* __restrict__ u, const float4* __restrict__ kf, TIO* __restrict__ y, int B,
                         int H, const h8* __restrict__ ftab, const float4* __restrict__ twtab) {
   constexpr int R0 = P::R0;
-  constexpr bool ROWS = P::row_loads(CH, NW);
-  constexpr int SCR_F4 = ROWS ? scratch_bytes<P, TIO>() / 16 : 0;
+  constexpr bool ROWS = P::row_loads(CH, NW), K1 = !ROWS;
+  constexpr int SCR_F4 = (ROWS ? scratch_bytes<P, TIO>() : P::out_scratch((int)sizeof(TIO))) / 16;
   constexpr bool SP_LDS = P::spectra_in_lds(CH, NW);
-  constexpr int SPL_F4 = SP_LDS ? CH * P::SP_F4 : 0;
-  __shared__ float4 lds[P::TAB_F4 + SPL_F4 + NW * SCR_F4];
+  constexpr int SPL_F4 = SP_LDS ? CH * P::SP_F4 : 0, TAB_F4 = P::tables_f4(CH, NW);
+  constexpr int F0_H8 = K1 ? P::F0_H8 / 2 : P::F0_H8, F1_H8 = K1 ? P::F1_H8 / 2 : P::F1_H8;
+  static_assert((TAB_F4 + SPL_F4 + NW * SCR_F4) * 16 <= P::lds_bytes(CH, NW), "layout within the plan's LDS");
+  __shared__ float4 lds[TAB_F4 + SPL_F4 + NW * SCR_F4];
   h8* F0 = reinterpret_cast<h8*>(lds);
-  h8* F1 = P::R1 == P::R0 ? F0 : F0 + P::F0_H8;
-  float4* TW1 = lds + P::F0_H8 + P::F1_H8;
+  h8* F1 = P::R1 == P::R0 ? F0 : F0 + F0_H8;
+  float4* TW1 = lds + F0_H8 + F1_H8;
   float4* TW2 = P::TW_TABLES == 2 ? TW1 + P::TW_F4 : TW1;
-  float4* SPL = lds + P::TAB_F4;
+  float4* SPL = lds + TAB_F4;
 
   // the wavefront index is uniform: read it into a scalar register so the pair and
   // channel arithmetic derived from it runs on the scalar unit
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  TIO* S = reinterpret_cast<TIO*>(lds + P::TAB_F4 + SPL_F4 + wave * SCR_F4);
+  TIO* S = reinterpret_cast<TIO*>(lds + TAB_F4 + SPL_F4 + wave * SCR_F4);
   const int BP = B >> 1, h0 = blockIdx.x * CH;
   const int nch = H - h0 < CH ? H - h0 : CH;  // channels of this workgroup
 
   // ---- tables and spectra: direct global -> LDS copies, issued first
   dma_to_lds<P::TW_TABLES * P::TW_F4, NW>(TW1, [&](int k) { return twtab + k; }, lane, wave);
   if constexpr (CACHED) {
-    dma_to_lds<P::F0_H8, NW>(reinterpret_cast<float4*>(F0), [&](int k) {
-      return reinterpret_cast<const float4*>(ftab + cf_off(R0) + k);
-    }, lane, wave);
+    // with K1 the first-kind runs only: LDS run i is table run 2i
+    auto tab = [&](int R, int k) {
+      return reinterpret_cast<const float4*>(ftab + cf_off(R) + (K1 ? ((k >> 6) << 7) + (k & 63) : k));
+    };
+    dma_to_lds<F0_H8, NW>(reinterpret_cast<float4*>(F0), [&](int k) { return tab(R0, k); }, lane, wave);
     if constexpr (P::R1 != P::R0)
-      dma_to_lds<P::F1_H8, NW>(reinterpret_cast<float4*>(F1), [&](int k) {
-        return reinterpret_cast<const float4*>(ftab + cf_off(P::R1) + k);
-      }, lane, wave);
+      dma_to_lds<F1_H8, NW>(reinterpret_cast<float4*>(F1), [&](int k) { return tab(P::R1, k); }, lane, wave);
   }
   if constexpr (SP_LDS) {
     // channel c of this workgroup is in slot c; slots past the last channel copy
@@ -527,8 +582,8 @@ __global__ void __launch_bounds__(64 * NW)
     else return kf + (size_t)(h0 + c) * P::SP_F4;
   };
   if constexpr (!CACHED) {
-    compute_dft<R0, 64 * NW>(F0, tid);
-    if constexpr (P::R1 != P::R0) compute_dft<P::R1, 64 * NW>(F1, tid);
+    compute_dft<R0, 64 * NW, K1>(F0, tid);
+    if constexpr (P::R1 != P::R0) compute_dft<P::R1, 64 * NW, K1>(F1, tid);
   }
 
   // ---- the first pairs. The waves of the first channel issue their loads right
