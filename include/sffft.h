@@ -1,6 +1,7 @@
 /* sffft.h - C ABI of the MI355X fused causal long-convolution library (libsffft.so).
  *
  *   y[b,h,n] = sum_{m<=n} u[b,h,m] * k[h,n-m],  n < L,  L a power of two in [128, 16384]
+ *   (single-pass plans) or in [2048, 131072] (multi-pass plans, sffft_conv_long_*)
  *
  * The reference has no library: its interface is two kernel launches inside
  * src/sffft.cu. Each entry point below names the reference code it replaces.
@@ -45,6 +46,10 @@ extern "C" {
  *               uploads its immutable twiddle table, 16*L bytes)
  *   channels : mode 1 only: channels per workgroup; their spectra are copied into
  *           LDS once and shared by the wavefronts of each channel (mode 0: 1)
+ *   mode 2 : multi-pass (sffft_conv_long_*): N = r0 * (r1 * r2), a column transform of
+ *           radix r0 and row transforms of length r1*r2 (the wave pipeline's two-stage
+ *           row plan), with the intermediate in a caller-provided workspace; waves = 4,
+ *           acc = 0, cached = 1, seqs = 2, channels = 1
  */
 typedef struct sffft_plan {
   int r0, r1, r2;
@@ -69,7 +74,8 @@ int sffft_plan_occupancy(int L, const sffft_plan* plan, int* blocks_per_cu);
 
 /* The plan registry used by the driver and the selector: the i-th compiled plan
  * for length L (acc = 0, cached = 1 are filled in; callers vary them; r*, waves,
- * seqs and mode identify the compiled kernel). Writes the plan name ("64x32") into
+ * seqs and mode identify the compiled kernel). For L > 16384 it lists the compiled
+ * multi-pass (mode 2) plans. Writes the plan name ("64x32") into
  * name. Returns SFFFT_ENOTFOUND past the end.
  * Replaces the RUN(...) plan table (src/sffft.cu:506-513). */
 int sffft_plan_count(int L);
@@ -99,6 +105,21 @@ int sffft_conv_f32(const float* u, const void* kf, float* y, int B, int H, int L
 /* bf16 I/O: u and y hold bf16 bit patterns; y is rounded to nearest even. */
 int sffft_conv_bf16(const uint16_t* u, const void* kf, uint16_t* y, int B, int H, int L,
                     const sffft_plan* plan, void* stream);
+
+/* Multi-pass convolution (mode-2 plans), for sequences whose length-2L transform does
+ * not fit one CU's LDS. No counterpart in the reference, which stops at L = 8192 and
+ * names a four-step split with an HBM pass as the way beyond (README.md:175). Three
+ * launches on `stream`: a column transform of radix r0 over the input, the row
+ * transforms with the spectrum product, and the inverse column transform. `work` is
+ * caller-owned device memory of at least sffft_work_bytes() bytes (the complex fp16
+ * intermediate, (B/2) * H * 2L * 4 bytes), 16-byte aligned and disjoint from u, y and
+ * kf; its contents are clobbered. kf comes from sffft_spectrum* with the same plan.
+ * B must be even (pairs of sequences). Same error codes as sffft_conv_*. */
+size_t sffft_work_bytes(int B, int H, int L, const sffft_plan* plan);  /* 0 if invalid or not mode 2 */
+int sffft_conv_long_f32(const float* u, const void* kf, float* y, void* work, size_t work_bytes, int B, int H, int L,
+                        const sffft_plan* plan, void* stream);
+int sffft_conv_long_bf16(const uint16_t* u, const void* kf, uint16_t* y, void* work, size_t work_bytes, int B, int H,
+                         int L, const sffft_plan* plan, void* stream);
 
 /* fp32 -> bf16 (round to nearest even) on the device. Replaces tobf16 (src/sffft.cu:306). */
 int sffft_to_bf16(const float* x, uint16_t* y, size_t n, void* stream);

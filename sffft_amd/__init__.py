@@ -21,12 +21,15 @@ HEADER_PATH = os.path.join(os.path.dirname(_HERE), "include", "sffft.h")
 
 SFFFT_OK, SFFFT_EINVAL, SFFFT_ENOPLAN, SFFFT_EHIP, SFFFT_ENOTFOUND = 0, 1, 2, 3, 4
 LENGTHS = (128, 256, 512, 1024, 2048, 4096, 8192, 16384)
+# multi-pass plans (mode 2) beyond one CU's LDS
+LONG_LENGTHS = (32768, 65536, 131072)
 
 
 class Plan(ctypes.Structure):
     """sffft_plan: N = 2L = r0*r1*r2 (r2 = 1 for two-stage plans). mode 0: one
     workgroup per transform; mode 1: one wavefront per pair of sequences, `channels`
-    channels per workgroup."""
+    channels per workgroup; mode 2: multi-pass, column radix r0 and row plan r1 x r2,
+    with a workspace (conv_long)."""
 
     _fields_ = [
         ("r0", ctypes.c_int),
@@ -101,6 +104,9 @@ def lib() -> ctypes.CDLL:
             "sffft_spectrum_from_natural": (ci, [vp, ci, ci, P, vp, vp]),
             "sffft_conv_f32": (ci, [vp, vp, vp, ci, ci, ci, P, vp]),
             "sffft_conv_bf16": (ci, [vp, vp, vp, ci, ci, ci, P, vp]),
+            "sffft_work_bytes": (sz, [ci, ci, ci, P]),
+            "sffft_conv_long_f32": (ci, [vp, vp, vp, vp, sz, ci, ci, ci, P, vp]),
+            "sffft_conv_long_bf16": (ci, [vp, vp, vp, vp, sz, ci, ci, ci, P, vp]),
             "sffft_to_bf16": (ci, [vp, vp, sz, vp]),
             "sffft_dispatch_floor": (ci, [ci, ci, ci, P, vp]),
             "sffft_dft_table": (ci, [vp, sz]),
@@ -157,13 +163,25 @@ DEFAULT_PLANS = {
     (8192, "fp32"): ("32x32x16", 8, 2, 0, 1), (8192, "bf16"): ("64x16x16", 8, 2, 0, 1),
     (16384, "fp32"): ("32x32x32", 16, 2, 0, 1), (16384, "bf16"): ("32x32x32", 16, 2, 0, 1),
 }
+# Multi-pass plans (mode 2): column radix x row plan, measured at B=8, H=768
+LONG_DEFAULT_PLANS = {32768: "64x32x32", 65536: "64x64x32", 131072: "64x64x64"}
 # One sequence per transform (workgroup kernel) for an odd batch
 ODD_BATCH_PLANS = {128: ("16x16", 2), 256: ("32x16", 2), 512: ("32x32", 2), 1024: ("64x32", 4),
                    2048: ("16x16x16", 8), 4096: ("32x16x16", 8), 8192: ("32x32x16", 4), 16384: ("32x32x32", 8)}
 
 
+def long_plan(spec: str) -> Plan:
+    """A multi-pass plan "NCxR0xR1": column radix NC, row plan R0 x R1."""
+    return make_plan(spec, 4, acc=0, cached=1, seqs=2, mode=2, channels=1)
+
+
 def default_plan(L: int, io: str = "fp32", B: int = 8, acc: int = 0) -> Plan:
-    """The tuned plan for length L and I/O type; pairs of sequences need an even B."""
+    """The tuned plan for length L and I/O type; pairs of sequences need an even B.
+    Beyond L = 16384 the plan is multi-pass (mode 2), which needs an even B and acc = 0."""
+    if L in LONG_DEFAULT_PLANS:
+        if B % 2 or acc:
+            raise ValueError(f"L={L}: multi-pass plans take pairs of sequences (even B) and fp32 accumulation")
+        return long_plan(LONG_DEFAULT_PLANS[L])
     spec, waves, seqs, mode, channels = DEFAULT_PLANS[(L, io)]
     if seqs == 2 and B % 2:
         spec, waves = ODD_BATCH_PLANS[L]
@@ -237,14 +255,23 @@ def spectrum_from_natural(kc, L: int, plan: Plan):
     return kf
 
 
-def conv(u, kf, plan: Plan, out=None):
-    """y = causal_conv(u, k) for u [B, H, L] fp32 or bf16 (cuda), kf from spectrum()."""
+def work_bytes(B: int, H: int, L: int, plan: Plan) -> int:
+    """Workspace bytes of a multi-pass (mode 2) plan; 0 for the other modes."""
+    return lib().sffft_work_bytes(B, H, L, ctypes.byref(plan))
+
+
+def conv(u, kf, plan: Plan, out=None, work=None):
+    """y = causal_conv(u, k) for u [B, H, L] fp32 or bf16 (cuda), kf from spectrum().
+    Multi-pass plans (mode 2) use `work` (a cuda tensor of at least work_bytes() bytes),
+    or allocate one for the call."""
     import torch
 
     assert u.is_cuda and u.dim() == 3
     u = u.contiguous()
     B, H, L = u.shape
     y = torch.empty_like(u) if out is None else out
+    if plan.mode == 2:
+        return conv_long(u, kf, plan, y, work)
     if u.dtype == torch.float32:
         fn = lib().sffft_conv_f32
     elif u.dtype == torch.bfloat16:
@@ -252,6 +279,28 @@ def conv(u, kf, plan: Plan, out=None):
     else:
         raise TypeError(f"unsupported dtype {u.dtype}")
     _check(fn(_ptr(u), _ptr(kf), _ptr(y), B, H, L, ctypes.byref(plan), _stream()), "sffft_conv")
+    return y
+
+
+def conv_long(u, kf, plan: Plan, out=None, work=None):
+    """Multi-pass convolution (sffft_conv_long_*): three launches on the current stream."""
+    import torch
+
+    u = u.contiguous()
+    B, H, L = u.shape
+    y = torch.empty_like(u) if out is None else out
+    nbytes = work_bytes(B, H, L, plan)
+    if work is None:
+        work = torch.empty(max(nbytes, 16), dtype=torch.uint8, device=u.device)
+    if u.dtype == torch.float32:
+        fn = lib().sffft_conv_long_f32
+    elif u.dtype == torch.bfloat16:
+        fn = lib().sffft_conv_long_bf16
+    else:
+        raise TypeError(f"unsupported dtype {u.dtype}")
+    wb = work.numel() * work.element_size()
+    _check(fn(_ptr(u), _ptr(kf), _ptr(y), _ptr(work), wb, B, H, L, ctypes.byref(plan), _stream()),
+           "sffft_conv_long")
     return y
 
 

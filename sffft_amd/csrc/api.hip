@@ -13,6 +13,7 @@
 #include "../../include/sffft.h"
 #include "fftconv.hpp"
 #include "fftconv_wave.hpp"
+#include "longconv.hpp"
 #include "registry.hpp"
 
 namespace sffft {
@@ -28,15 +29,26 @@ int hip_status(hipError_t err, const char* what) {
 }
 
 bool valid_radix(int r) { return r == 16 || r == 32 || r == 64; }
-bool valid_length(int L) { return L >= 128 && L <= 16384 && (L & (L - 1)) == 0; }
-// mode 0: 1, 2, 4, 8 or 16 wavefronts; mode 1 (one pair per wavefront): 1..16
+// single-pass plans (modes 0 and 1) up to L = 16384; multi-pass plans (mode 2) up to
+// L = 131072 (N = 64 * 64 * 64)
+constexpr int MAX_SINGLE_L = 16384, MAX_LONG_L = 131072;
+bool valid_length(int L) { return L >= 128 && L <= MAX_LONG_L && (L & (L - 1)) == 0; }
+// mode 0: 1, 2, 4, 8 or 16 wavefronts; mode 1 (one pair per wavefront): 1..16;
+// mode 2: the four wavefronts of every pass
 bool valid_waves(int w, int mode) {
+  if (mode == 2) return w == LC_WAVES;
   return mode == 1 ? (w >= 1 && w <= 16) : (w == 1 || w == 2 || w == 4 || w == 8 || w == 16);
 }
 
 // Same formulas as Plan<>::LDS_BYTES and WavePlan<>::LDS_BYTES, for plans that are
 // not compiled.
 size_t lds_bytes_rt(int r0, int r1, int r2, int mode, int channels, int waves) {
+  if (mode == 2) {
+    // LongRowPlan::LDS_BYTES of the row plan r1 x r2: first-kind DFT fragments and the
+    // twiddle table(s)
+    const int T1 = r1 / 16, T2 = r2 / 16, NR = r1 * r2;
+    return (size_t)(T1 * T1 * 64 + (r2 == r1 ? 0 : T2 * T2 * 64)) * 16 + (size_t)(r2 == r1 ? 1 : 2) * NR * 8;
+  }
   if (mode == 1) {
     // WavePlan::lds_bytes: DFT fragments and the twiddle tables (one when r0 == r1);
     // then, in order of preference, row-load scratch and spectra; strided loads with
@@ -79,10 +91,15 @@ const Entry* entries_for(int L, int* n) {
 
 int check_shape(int L, const sffft_plan* p) {
   if (!p || !valid_length(L)) return SFFFT_EINVAL;
+  if (p->mode != 2 && L > MAX_SINGLE_L) return SFFFT_EINVAL;
   if (!valid_radix(p->r0) || !valid_radix(p->r1) || !(p->r2 == 1 || valid_radix(p->r2))) return SFFFT_EINVAL;
   if ((long long)p->r0 * p->r1 * p->r2 != 2LL * L) return SFFFT_EINVAL;
   if (!valid_waves(p->waves, p->mode) || (p->acc != 0 && p->acc != 1) || (p->cached != 0 && p->cached != 1) ||
-      (p->seqs != 1 && p->seqs != 2) || (p->mode != 0 && p->mode != 1) || p->channels < 1 || p->channels > 16)
+      (p->seqs != 1 && p->seqs != 2) || p->mode < 0 || p->mode > 2 || p->channels < 1 || p->channels > 16)
+    return SFFFT_EINVAL;
+  // multi-pass: three radices (column radix r0, row plan r1 x r2), pairs of sequences,
+  // fp32 accumulation, DFT fragments from the coefficient table
+  if (p->mode == 2 && (p->r2 == 1 || p->seqs != 2 || p->channels != 1 || p->acc != 0 || p->cached != 1))
     return SFFFT_EINVAL;
   if (p->mode == 0 && p->channels != 1) return SFFFT_EINVAL;
   if (p->mode == 1 && (p->r2 != 1 || p->seqs != 2)) return SFFFT_EINVAL;
@@ -91,7 +108,17 @@ int check_shape(int L, const sffft_plan* p) {
   return SFFFT_OK;
 }
 
+const LongEntry* find_long_entry(const sffft_plan* p) {
+  if (p->mode != 2) return nullptr;
+  int n = 0;
+  const LongEntry* e = long_entries(&n);
+  for (int i = 0; i < n; i++)
+    if (e[i].nc == p->r0 && e[i].r0 == p->r1 && e[i].r1 == p->r2) return &e[i];
+  return nullptr;
+}
+
 const Entry* find_entry(int L, const sffft_plan* p) {
+  if (p->mode == 2) return nullptr;
   int n = 0;
   const Entry* e = entries_for(L, &n);
   for (int i = 0; i < n; i++)
@@ -318,9 +345,17 @@ __global__ void spectrum_permute_kernel(const float2* __restrict__ src, float2* 
   const size_t gid = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (gid >= (size_t)H * N) return;
   const int h = (int)(gid / N), idx = (int)(gid % N);
-  int k0, k1, k2;
-  kernel_order_digits_rt(idx, r0, r1, r2, mode, k0, k1, k2);
-  const int s = natural ? k0 + r0 * k1 + r0 * r1 * k2 : k0 * (r1 * r2) + k1 * r2 + k2;
+  int k0, k1, k2, s;
+  if (mode == 2) {
+    // multi-pass: row k1 = idx / NR holds the row plan's spectrum order (the wave
+    // pipeline's sp_index over the row plan r1 x r2) of frequencies k1 + r0*(k0' + r1*k1')
+    const int NR = r1 * r2, row = idx / NR;
+    kernel_order_digits_rt(idx - row * NR, r1, r2, 1, 1, k0, k1, k2);
+    s = natural ? row + r0 * (k0 + r1 * k1) : row * NR + k0 * r2 + k1;
+  } else {
+    kernel_order_digits_rt(idx, r0, r1, r2, mode, k0, k1, k2);
+    s = natural ? k0 + r0 * k1 + r0 * r1 * k2 : k0 * (r1 * r2) + k1 * r2 + k2;
+  }
   const float2 v = src[(size_t)h * N + s];
   kf[gid] = make_float2(v.x * scale, v.y * scale);
 }
@@ -334,6 +369,8 @@ __global__ void to_bf16_kernel(const float* __restrict__ x, uint16_t* __restrict
 // wave plans also carry the 1/sqrt(R1) of their shared twiddle table (1/R1 in all).
 float last_stage_scale(const sffft_plan* p) {
   const int R = p->r2 > 1 ? p->r2 : p->r1;
+  // multi-pass: the row plan r1 x r2's factor (its forward DFT over n1 of radix r2)
+  if (p->mode == 2) return (float)(p->r1 == p->r2 ? 1.0 / (double)R : 1.0 / std::sqrt((double)R));
   if (p->mode == 1 && p->r0 == p->r1) return (float)(1.0 / (double)R);
   return (float)(1.0 / std::sqrt((double)R));
 }
@@ -351,6 +388,7 @@ int conv(const void* u, const void* kf, void* y, int B, int H, int L, const sfff
   int rc = check_shape(L, p);
   if (rc) return rc;
   if (B % p->seqs) return SFFFT_EINVAL;
+  if (p->mode == 2) return SFFFT_EINVAL;  // multi-pass plans need a workspace: sffft_conv_long_*
   if (!aligned16(u) || !aligned16(y) || !aligned16(kf)) return SFFFT_EINVAL;
   const Entry* e = find_entry(L, p);
   if (!e) return SFFFT_ENOPLAN;
@@ -360,6 +398,50 @@ int conv(const void* u, const void* kf, void* y, int B, int H, int L, const sfff
   if (e->mode == 1 && (rc = device_twiddles(p->r0, p->r1, &tw))) return rc;
   return hip_status(e->launch[IO][p->cached](u, kf, y, B, H, table, tw, p->acc, (hipStream_t)stream),
                     "fused convolution launch");
+}
+
+size_t work_bytes(int B, int H, int L) { return (size_t)(B / 2) * H * 2 * L * 4; }
+
+template <int IO>
+int conv_long(const void* u, const void* kf, void* y, void* work, size_t wbytes, int B, int H, int L,
+              const sffft_plan* p, void* stream) {
+  if (!u || !kf || !y || !work || B < 2 || H < 1 || (long long)B * H > INT_MAX) return SFFFT_EINVAL;
+  int rc = check_shape(L, p);
+  if (rc) return rc;
+  if (p->mode != 2 || B % 2) return SFFFT_EINVAL;
+  if (!aligned16(u) || !aligned16(y) || !aligned16(kf) || !aligned16(work)) return SFFFT_EINVAL;
+  if (wbytes < work_bytes(B, H, L)) return SFFFT_EINVAL;
+  // row counts of the passes are int
+  if ((long long)H * p->r0 * (B / 2) > INT_MAX || (long long)(B / 2) * H * (p->r1 * p->r2 / LC_CBLOCK) > INT_MAX)
+    return SFFFT_EINVAL;
+  // the workspace must not overlap the input, output or spectrum
+  auto overlaps = [](const void* a, size_t na, const void* b, size_t nb) {
+    const uintptr_t x = (uintptr_t)a, z = (uintptr_t)b;
+    return x < z + nb && z < x + na;
+  };
+  const size_t io_bytes = (size_t)B * H * L * (IO ? 2 : 4);
+  if (overlaps(work, wbytes, u, io_bytes) || overlaps(work, wbytes, y, io_bytes) ||
+      overlaps(work, wbytes, kf, (size_t)H * 2 * L * 8))
+    return SFFFT_EINVAL;
+  const LongEntry* e = find_long_entry(p);
+  if (!e) return SFFFT_ENOPLAN;
+  const void* table = nullptr;
+  if ((rc = device_table(&table))) return rc;
+  const void* tw = nullptr;
+  if ((rc = device_twiddles(p->r1, p->r2, &tw))) return rc;
+  return hip_status(e->launch[IO](u, kf, y, work, B, H, table, tw, (hipStream_t)stream), "multi-pass launch");
+}
+
+// Compiled multi-pass plans of length L, in registry order.
+int long_plans_for(int L, const LongEntry** out, int cap) {
+  int n = 0, k = 0;
+  const LongEntry* e = long_entries(&n);
+  for (int i = 0; i < n; i++)
+    if ((long long)e[i].nc * e[i].r0 * e[i].r1 == 2LL * L) {
+      if (k < cap) out[k] = &e[i];
+      k++;
+    }
+  return k;
 }
 
 }  // namespace
@@ -372,6 +454,7 @@ extern "C" {
 int sffft_plan_check(int L, const sffft_plan* plan) {
   const int rc = check_shape(L, plan);
   if (rc) return rc;
+  if (plan->mode == 2) return find_long_entry(plan) ? SFFFT_OK : SFFFT_ENOPLAN;
   return find_entry(L, plan) ? SFFFT_OK : SFFFT_ENOPLAN;
 }
 
@@ -385,9 +468,10 @@ int sffft_plan_occupancy(int L, const sffft_plan* plan, int* blocks_per_cu) {
   const int rc = sffft_plan_check(L, plan);
   if (rc) return rc;
   const Entry* e = find_entry(L, plan);
+  const void* func = plan->mode == 2 ? find_long_entry(plan)->rows_func : e->func[0][plan->cached];
   int n = 0;
   const int st = hip_status(
-      hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, e->func[0][plan->cached], 64 * plan->waves, 0),
+      hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, func, 64 * plan->waves, 0),
       "hipOccupancyMaxActiveBlocksPerMultiprocessor");
   if (st) return st;
   *blocks_per_cu = n;
@@ -395,12 +479,21 @@ int sffft_plan_occupancy(int L, const sffft_plan* plan, int* blocks_per_cu) {
 }
 
 int sffft_plan_count(int L) {
+  if (L > MAX_SINGLE_L) return valid_length(L) ? long_plans_for(L, nullptr, 0) : 0;
   int n = 0;
   entries_for(L, &n);
   return n;
 }
 
 int sffft_plan_get(int L, int index, sffft_plan* plan, char* name, size_t name_len) {
+  if (L > MAX_SINGLE_L) {
+    const LongEntry* le[64];
+    const int n = valid_length(L) ? long_plans_for(L, le, 64) : 0;
+    if (index < 0 || index >= n || index >= 64) return SFFFT_ENOTFOUND;
+    if (plan) *plan = sffft_plan{le[index]->nc, le[index]->r0, le[index]->r1, LC_WAVES, 0, 1, 2, 2, 1};
+    if (name && name_len) snprintf(name, name_len, "%dx%dx%d", le[index]->nc, le[index]->r0, le[index]->r1);
+    return SFFFT_OK;
+  }
   int n = 0;
   const Entry* e = entries_for(L, &n);
   if (index < 0 || index >= n) return SFFFT_ENOTFOUND;
@@ -472,11 +565,26 @@ int sffft_conv_bf16(const uint16_t* u, const void* kf, uint16_t* y, int B, int H
   return conv<1>(u, kf, y, B, H, L, plan, stream);
 }
 
+size_t sffft_work_bytes(int B, int H, int L, const sffft_plan* plan) {
+  if (B < 2 || B % 2 || H < 1 || check_shape(L, plan) || plan->mode != 2) return 0;
+  return work_bytes(B, H, L);
+}
+
+int sffft_conv_long_f32(const float* u, const void* kf, float* y, void* work, size_t work_bytes, int B, int H, int L,
+                        const sffft_plan* plan, void* stream) {
+  return conv_long<0>(u, kf, y, work, work_bytes, B, H, L, plan, stream);
+}
+
+int sffft_conv_long_bf16(const uint16_t* u, const void* kf, uint16_t* y, void* work, size_t work_bytes, int B, int H,
+                         int L, const sffft_plan* plan, void* stream) {
+  return conv_long<1>(u, kf, y, work, work_bytes, B, H, L, plan, stream);
+}
+
 int sffft_dispatch_floor(int B, int H, int L, const sffft_plan* plan, void* stream) {
   if (B < 1 || H < 1 || (long long)B * H > INT_MAX) return SFFFT_EINVAL;
   int rc = check_shape(L, plan);
   if (rc) return rc;
-  if (B % plan->seqs) return SFFFT_EINVAL;
+  if (B % plan->seqs || plan->mode == 2) return SFFFT_EINVAL;
   const Entry* e = find_entry(L, plan);
   if (!e) return SFFFT_ENOPLAN;
   const unsigned grid = e->mode == 1 ? (unsigned)((H + e->channels - 1) / e->channels)

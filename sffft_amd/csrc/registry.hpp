@@ -32,4 +32,16 @@ const Entry* entries_L4096(int* n);
 const Entry* entries_L8192(int* n);
 const Entry* entries_L16384(int* n);
 
+// Multi-pass plans (mode 2, longconv.hpp): column radix nc, row plan r0 x r1; the three
+// passes run on one stream with the caller's workspace.
+typedef hipError_t (*long_launch_fn)(const void* u, const void* kf, void* y, void* work, int B, int H,
+                                     const void* ftab, const void* tw, hipStream_t stream);
+struct LongEntry {
+  int nc, r0, r1, lds_bytes;  // lds_bytes: the row pass's tables
+  long_launch_fn launch[2];   // [io: 0 = fp32, 1 = bf16]
+  const void* rows_func;      // the row-pass kernel (occupancy queries)
+};
+// Defined by long_inst.hip.
+const LongEntry* long_entries(int* n);
+
 }  // namespace sffft

@@ -76,3 +76,68 @@ def test_conv_argument_errors_need_no_gpu():
 def test_strerror():
     assert sf.strerror(sf.SFFFT_OK) == "success"
     assert "invalid" in sf.strerror(sf.SFFFT_EINVAL)
+
+
+def _long_plans_all():
+    for L in (2048, 4096, 8192, 16384) + sf.LONG_LENGTHS:
+        for nc in (16, 32, 64):
+            for rows in ((16, 16), (32, 32), (64, 32), (64, 64)):
+                if nc * rows[0] * rows[1] == 2 * L:
+                    yield L, sf.long_plan(f"{nc}x{rows[0]}x{rows[1]}")
+
+
+def test_long_plans_registry():
+    # every compiled multi-pass plan: column radix in {16, 32, 64} with one of four row plans
+    cases = list(_long_plans_all())
+    assert len(cases) == 12
+    for L, p in cases:
+        assert sf.plan_check(L, p) == sf.SFFFT_OK, (L, p)
+        NR = p.r1 * p.r2
+        frags = ((p.r1 // 16) ** 2 + (0 if p.r1 == p.r2 else (p.r2 // 16) ** 2)) * 64 * 16
+        assert sf.lds_bytes(L, p) == frags + (1 if p.r1 == p.r2 else 2) * NR * 8
+        assert sf.work_bytes(8, 768, L, p) == 4 * 768 * 2 * L * 4
+    for L in sf.LONG_LENGTHS:
+        listed = sf.plans(L)
+        assert listed and all(q.mode == 2 and q.r0 * q.r1 * q.r2 == 2 * L for q in listed)
+        assert repr(sf.default_plan(L)) in [repr(q) for q in listed]
+    assert sf.lib().sffft_plan_count(262144) == 0
+    assert sf.lib().sffft_spectrum_bytes(768, 131072) == 768 * 262144 * 8
+
+
+def test_long_plan_validation():
+    P, LP = sf.make_plan, sf.long_plan
+    assert sf.plan_check(65536, LP("32x64x64")) == sf.SFFFT_OK
+    assert sf.plan_check(65536, LP("32x64x64").replace(acc=1)) == sf.SFFFT_EINVAL     # fp32 accumulation only
+    assert sf.plan_check(65536, LP("32x64x64").replace(cached=0)) == sf.SFFFT_EINVAL  # table fragments only
+    assert sf.plan_check(65536, LP("32x64x64").replace(seqs=1)) == sf.SFFFT_EINVAL    # pairs only
+    assert sf.plan_check(65536, LP("32x64x64").replace(waves=8)) == sf.SFFFT_EINVAL
+    assert sf.plan_check(65536, LP("64x32x64")) == sf.SFFFT_ENOPLAN                   # row plan not compiled
+    assert sf.plan_check(65536, LP("64x64x64")) == sf.SFFFT_EINVAL                    # product != 2L
+    assert sf.plan_check(65536, P("32x64x64", 8)) == sf.SFFFT_EINVAL                  # single-pass beyond 16384
+    assert sf.plan_check(262144, LP("64x64x64")) == sf.SFFFT_EINVAL                   # beyond 131072
+    assert sf.work_bytes(7, 768, 65536, LP("32x64x64")) == 0                          # odd B
+    assert sf.work_bytes(8, 768, 1024, sf.make_plan("64x32", 4, seqs=2)) == 0         # not multi-pass
+
+
+def test_long_conv_argument_errors_need_no_gpu():
+    p = sf.long_plan("32x64x64")
+    lib = sf.lib()
+    null = ctypes.c_void_p(0)
+    L, B, H = 65536, 8, 4
+    need = sf.work_bytes(B, H, L, p)
+    io = B * H * L * 4
+    u, kf, y, w = (ctypes.c_void_p((1 << 40) + i * (1 << 34)) for i in range(4))
+    f = lib.sffft_conv_long_f32
+    assert f(u, kf, y, null, need, B, H, L, ctypes.byref(p), null) == sf.SFFFT_EINVAL          # no workspace
+    assert f(u, kf, y, w, need - 1, B, H, L, ctypes.byref(p), null) == sf.SFFFT_EINVAL         # too small
+    assert f(u, kf, y, w, need, 7, H, L, ctypes.byref(p), null) == sf.SFFFT_EINVAL            # B odd
+    assert f(u, kf, y, ctypes.c_void_p((1 << 40) + 8), need, B, H, L, ctypes.byref(p),
+             null) == sf.SFFFT_EINVAL                                                         # misaligned
+    assert f(u, kf, y, ctypes.c_void_p((1 << 40) + io - 16), need, B, H, L, ctypes.byref(p),
+             null) == sf.SFFFT_EINVAL                                                         # overlaps u
+    assert f(u, kf, y, w, need, B, H, 1024, ctypes.byref(p), null) == sf.SFFFT_EINVAL          # plan vs L
+    single = sf.make_plan("64x32", 4, seqs=2)
+    assert f(u, kf, y, w, need, B, H, 1024, ctypes.byref(single), null) == sf.SFFFT_EINVAL     # not mode 2
+    # the single-pass entry points refuse a multi-pass plan (it needs a workspace)
+    assert lib.sffft_conv_f32(u, kf, y, B, H, L, ctypes.byref(p), null) == sf.SFFFT_EINVAL
+    assert lib.sffft_dispatch_floor(B, H, L, ctypes.byref(p), null) == sf.SFFFT_EINVAL

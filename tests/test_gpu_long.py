@@ -1,0 +1,126 @@
+"""Parity of the multi-pass convolution (mode-2 plans, sffft_conv_long_*) with the fp64
+oracle, through the C ABI.
+
+Every compiled plan (column radix 16, 32 or 64 with row plans 16x16, 32x32, 64x32 and
+64x64, L = 2048 .. 131072) runs both I/O types on seeded inputs and is compared over all
+outputs with the oracle's fp64 FFT convolution (direct convolution at L = 2048). Bounds
+are those of the fused kernel: 5e-4 for fp32 I/O (6e-4 is not needed: the pass-A input
+enters as an fp16 value plus its remainder) and 3e-3 for bf16 I/O, whose error includes
+the rounding of inputs and outputs.
+
+At the plans' own small L the result must also agree with the single-pass kernel to
+the same bound, and the bench configurations run at full B=8, H=768 through the
+bit-exact properties of test_gpu_configs.py (permutation of pairs and channels,
+repeatability) on sampled sequences.
+"""
+import numpy as np
+import pytest
+
+import oracle
+import sffft_amd as sf
+
+pytestmark = pytest.mark.gpu
+
+BOUND = {"fp32": 5e-4, "bf16": 3e-3}
+
+
+def _cases():
+    for L in (2048, 4096, 8192, 16384) + sf.LONG_LENGTHS:
+        for nc in (16, 32, 64):
+            for rows in ((16, 16), (32, 32), (64, 32), (64, 64)):
+                if nc * rows[0] * rows[1] == 2 * L:
+                    yield L, f"{nc}x{rows[0]}x{rows[1]}"
+
+
+def _run(dev, u, k, plan, io, work=None):
+    import torch
+
+    L = u.shape[-1]
+    kf = sf.spectrum(torch.from_numpy(k).to(dev), L, plan)
+    ud = torch.from_numpy(u).to(dev)
+    if io == "bf16":
+        ud = sf.to_bf16(ud)
+    y = sf.conv(ud, kf, plan, work=work)
+    torch.cuda.synchronize()
+    return y.float().cpu().numpy()
+
+
+@pytest.mark.parametrize("L,spec", list(_cases()))
+def test_long_conv_matches_oracle(dev, L, spec):
+    plan = sf.long_plan(spec)
+    # B=6 (three pairs per channel: a workgroup's last row slot idle), H=3; fewer rows
+    # at the longest lengths
+    B, H = (6, 3) if L <= 16384 else (4, 2)
+    u, k = oracle.gen_inputs(B, H, L, seed=L + plan.r0)
+    ref = oracle.conv(u, k)
+    for io in ("fp32", "bf16"):
+        print(f"case L={L} {spec} io={io} B={B} H={H}", flush=True)
+        y = _run(dev, u, k, plan, io)
+        err = oracle.rel_l2(y, ref)
+        print(f"  rel_l2={err:.3e}", flush=True)
+        assert np.isfinite(err) and err <= BOUND[io], (L, spec, io, err)
+
+
+def test_long_matches_single_pass(dev):
+    # one pair per channel (B=2): the row pass's workgroups take rows of different channels
+    L, B, H = 8192, 2, 5
+    u, k = oracle.gen_inputs(B, H, L, seed=11)
+    ref = oracle.conv(u, k)
+    a = _run(dev, u, k, sf.long_plan("64x16x16"), "fp32")
+    b = _run(dev, u, k, sf.default_plan(L, "fp32", B), "fp32")
+    assert oracle.rel_l2(a, ref) <= 5e-4 and oracle.rel_l2(b, ref) <= 6e-4
+    assert oracle.rel_l2(a, b.astype(np.float64)) <= 1e-3
+
+
+def test_long_workspace_reuse_and_delta(dev):
+    """A caller's workspace is reused across calls (it is fully rewritten), and closed
+    forms hold: a unit impulse at n = 0 in u returns k itself; a shifted impulse returns
+    the shifted filter (the oracle is not involved)."""
+    import torch
+
+    L, B, H = 32768, 2, 2
+    plan = sf.long_plan("64x32x32")
+    rng = np.random.default_rng(5)
+    k = (rng.standard_normal((H, L)) * np.exp(-np.arange(L) / 4096.0) / np.sqrt(L)).astype(np.float32)
+    u = np.zeros((B, H, L), np.float32)
+    u[0, :, 0] = 1.0
+    u[1, :, 777] = 1.0
+    work = torch.full((sf.work_bytes(B, H, L, plan),), 0x7f, dtype=torch.uint8, device=dev)
+    y1 = _run(dev, u, k, plan, "fp32", work=work)
+    y2 = _run(dev, u, k, plan, "fp32", work=work)
+    assert np.array_equal(y1, y2)
+    exp = np.zeros((B, H, L))
+    exp[0] = k
+    exp[1, :, 777:] = k[:, :L - 777]
+    assert oracle.rel_l2(y1, exp) <= 5e-4
+
+
+def test_long_full_batch_properties(dev):
+    """B=8, H=768, L=32768 fp32 with the default plan: sampled sequences against the
+    oracle; swapping two batch pairs permutes the output bit for bit; two launches
+    agree bit for bit."""
+    import torch
+
+    L, B, H = 32768, 8, 768
+    plan = sf.default_plan(L, "fp32", B)
+    g = torch.Generator(device=dev).manual_seed(3)
+    u = torch.randn((B, H, L), generator=g, device=dev, dtype=torch.float32)
+    n = torch.arange(L, device=dev, dtype=torch.float32)
+    k = torch.randn((H, L), generator=g, device=dev) * torch.exp(-n / 2048.0) / L ** 0.5
+    kf = sf.spectrum(k, L, plan)
+    work = torch.empty(sf.work_bytes(B, H, L, plan), dtype=torch.uint8, device=dev)
+    y = sf.conv(u, kf, plan, work=work)
+    y2 = sf.conv(u, kf, plan, work=work)
+    us = u[[2, 3, 0, 1, 4, 5, 6, 7]].contiguous()
+    ys = sf.conv(us, kf, plan, work=work)
+    torch.cuda.synchronize()
+    assert torch.equal(y, y2)
+    assert torch.equal(ys, y[[2, 3, 0, 1, 4, 5, 6, 7]])
+    rng = np.random.default_rng(0)
+    hs = rng.choice(H, 12, replace=False)
+    for b in (0, 5):
+        us_np = u[b, hs].cpu().numpy()[None]
+        ref = oracle.conv(us_np, k[hs].cpu().numpy())
+        err = oracle.rel_l2(y[b, hs].cpu().numpy()[None], ref)
+        print(f"  b={b} sampled rel_l2={err:.3e}", flush=True)
+        assert err <= 5e-4
