@@ -47,6 +47,8 @@ def parse():
     ap.add_argument("--cpu-baseline", type=int, default=1, help="time the fp64 CPU baseline (rank 0, N=1)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU sample budget (seconds)")
     ap.add_argument("--check", type=int, default=1, help="verify the output against the fp64 oracle")
+    ap.add_argument("--work-mb", type=float, default=0.0,
+                    help="multi-pass plans: workspace size in MB (0: the library's default chunking)")
     ap.add_argument("--copy-mb", type=float, default=0.0,
                     help="instead of the convolution, time a plain device-to-device copy of this many MB "
                          "(bandwidth reference and the calibration run for HBM byte counters)")
@@ -155,7 +157,10 @@ def main():
         y = torch.empty_like(u)
         sets.append((u, kf, y, k, u32 if i == 0 else None))
     # multi-pass plans: one workspace for every step (the steps run in stream order)
-    work = torch.empty(sf.work_bytes(B, H, L, plan), dtype=torch.uint8, device=dev) if plan.mode == 2 else None
+    work = None
+    if plan.mode == 2:
+        wb = int(a.work_mb * 1e6) if a.work_mb > 0 else sf.work_bytes(B, H, L, plan)
+        work = torch.empty(wb, dtype=torch.uint8, device=dev)
     torch.cuda.synchronize()
 
     def step(i):
@@ -295,6 +300,7 @@ def main():
                             "multi-pass: columns, rows, columns; complex fp16 workspace")[plan.mode],
                    "channels_per_workgroup": plan.channels,
                    "acc": "fp16" if plan.acc else "fp32", "rotated_sets": nsets,
+                   "workspace_bytes": None if work is None else work.numel(),
                    "rotated_bytes": nsets * set_bytes},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4),

@@ -109,13 +109,16 @@ int sffft_conv_bf16(const uint16_t* u, const void* kf, uint16_t* y, int B, int H
 /* Multi-pass convolution (mode-2 plans), for sequences whose length-2L transform does
  * not fit one CU's LDS. No counterpart in the reference, which stops at L = 8192 and
  * names a four-step split with an HBM pass as the way beyond (README.md:175). Three
- * launches on `stream`: a column transform of radix r0 over the input, the row
- * transforms with the spectrum product, and the inverse column transform. `work` is
- * caller-owned device memory of at least sffft_work_bytes() bytes (the complex fp16
- * intermediate, (B/2) * H * 2L * 4 bytes), 16-byte aligned and disjoint from u, y and
- * kf; its contents are clobbered. kf comes from sffft_spectrum* with the same plan.
- * B must be even (pairs of sequences). Same error codes as sffft_conv_*. */
-size_t sffft_work_bytes(int B, int H, int L, const sffft_plan* plan);  /* 0 if invalid or not mode 2 */
+ * launches on `stream` per chunk of channels: a column transform of radix r0 over the
+ * input, the row transforms with the spectrum product, and the inverse column transform.
+ * `work` is caller-owned device memory (the complex fp16 intermediate), 16-byte aligned
+ * and disjoint from u, y and kf, of work_bytes >= (B/2) * 2L * 4 bytes (one channel);
+ * the batch runs in chunks of floor(work_bytes / that) channels and the contents are
+ * clobbered. kf comes from sffft_spectrum* with the same plan. B must be even (pairs of
+ * sequences). Same error codes as sffft_conv_*. */
+/* The default workspace: chunks of at most 96 MiB, which stay in the 256 MB Infinity
+ * Cache between the passes (the whole batch if smaller). 0 if invalid or not mode 2. */
+size_t sffft_work_bytes(int B, int H, int L, const sffft_plan* plan);
 int sffft_conv_long_f32(const float* u, const void* kf, float* y, void* work, size_t work_bytes, int B, int H, int L,
                         const sffft_plan* plan, void* stream);
 int sffft_conv_long_bf16(const uint16_t* u, const void* kf, uint16_t* y, void* work, size_t work_bytes, int B, int H,

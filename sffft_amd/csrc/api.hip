@@ -400,7 +400,18 @@ int conv(const void* u, const void* kf, void* y, int B, int H, int L, const sfff
                     "fused convolution launch");
 }
 
-size_t work_bytes(int B, int H, int L) { return (size_t)(B / 2) * H * 2 * L * 4; }
+// Workspace of one channel (its B/2 pairs of 2L complex fp16 points); a workspace of
+// c channels runs the batch in ceil(H/c) chunks.
+size_t channel_work_bytes(int B, int L) { return (size_t)(B / 2) * 2 * L * 4; }
+// Default workspace: chunks of at most 96 MiB (kept in the 256 MB Infinity Cache
+// between the passes), or the whole batch when it is smaller.
+size_t work_bytes(int B, int H, int L) {
+  const size_t per = channel_work_bytes(B, L), cap = (size_t)96 << 20;
+  size_t ch = cap / per;
+  if (ch < 1) ch = 1;
+  if (ch > (size_t)H) ch = (size_t)H;
+  return ch * per;
+}
 
 template <int IO>
 int conv_long(const void* u, const void* kf, void* y, void* work, size_t wbytes, int B, int H, int L,
@@ -410,7 +421,9 @@ int conv_long(const void* u, const void* kf, void* y, void* work, size_t wbytes,
   if (rc) return rc;
   if (p->mode != 2 || B % 2) return SFFFT_EINVAL;
   if (!aligned16(u) || !aligned16(y) || !aligned16(kf) || !aligned16(work)) return SFFFT_EINVAL;
-  if (wbytes < work_bytes(B, H, L)) return SFFFT_EINVAL;
+  if (wbytes < channel_work_bytes(B, L)) return SFFFT_EINVAL;
+  const size_t chunk_sz = wbytes / channel_work_bytes(B, L);
+  const int chunk = chunk_sz < (size_t)H ? (int)chunk_sz : H;
   // row counts of the passes are int
   if ((long long)H * p->r0 * (B / 2) > INT_MAX || (long long)(B / 2) * H * (p->r1 * p->r2 / LC_CBLOCK) > INT_MAX)
     return SFFFT_EINVAL;
@@ -420,6 +433,7 @@ int conv_long(const void* u, const void* kf, void* y, void* work, size_t wbytes,
     return x < z + nb && z < x + na;
   };
   const size_t io_bytes = (size_t)B * H * L * (IO ? 2 : 4);
+  wbytes = (size_t)chunk * channel_work_bytes(B, L);  // the part the passes use
   if (overlaps(work, wbytes, u, io_bytes) || overlaps(work, wbytes, y, io_bytes) ||
       overlaps(work, wbytes, kf, (size_t)H * 2 * L * 8))
     return SFFFT_EINVAL;
@@ -429,7 +443,8 @@ int conv_long(const void* u, const void* kf, void* y, void* work, size_t wbytes,
   if ((rc = device_table(&table))) return rc;
   const void* tw = nullptr;
   if ((rc = device_twiddles(p->r1, p->r2, &tw))) return rc;
-  return hip_status(e->launch[IO](u, kf, y, work, B, H, table, tw, (hipStream_t)stream), "multi-pass launch");
+  return hip_status(e->launch[IO](u, kf, y, work, B, H, chunk, table, tw, (hipStream_t)stream),
+                    "multi-pass launch");
 }
 
 // Compiled multi-pass plans of length L, in registry order.

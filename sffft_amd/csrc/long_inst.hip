@@ -35,27 +35,33 @@ static unsigned rows_grid(int nrows) {
   return (unsigned)(need < n ? need : n);
 }
 
-// The three passes on one stream. work: (B/2)*H*N complex fp16 points.
+// The three passes on one stream, for chunks of `chunk` channels: the workspace holds
+// chunk*(B/2) pairs of N complex fp16 points.
 template <int NC, int R0, int R1, class TIO>
-static hipError_t launch_long(const void* u, const void* kf, void* y, void* work, int B, int H, const void* ftab,
-                              const void* tw, hipStream_t s) {
+static hipError_t launch_long(const void* u, const void* kf, void* y, void* work, int B, int H, int chunk,
+                              const void* ftab, const void* tw, hipStream_t s) {
   constexpr int NR = R0 * R1, N = NC * NR;
   const float inv_n = 1.0f / (float)N;  // exact: N is a power of two
   const int BP = B / 2;
-  const unsigned cgrid = (unsigned)((size_t)BP * H * (NR / LC_CBLOCK));
-  hipLaunchKernelGGL((long_cols_fwd<NC, TIO>), dim3(cgrid), dim3(64 * LC_WAVES), 0, s, static_cast<const TIO*>(u),
-                     static_cast<uint32_t*>(work), B, H, NR, inv_n, static_cast<const h8*>(ftab));
-  hipError_t err = hipGetLastError();
-  if (err != hipSuccess) return err;
-  const int nrows = H * NC * BP;
-  hipLaunchKernelGGL((long_rows<R0, R1>), dim3(rows_grid<R0, R1>(nrows)), dim3(64 * LC_WAVES), 0, s,
-                     static_cast<uint32_t*>(work), static_cast<const float4*>(kf), nrows, BP, NC, inv_n,
-                     inv_sqrt_radix<NC>(), static_cast<const h8*>(ftab), static_cast<const float4*>(tw));
-  if ((err = hipGetLastError()) != hipSuccess) return err;
-  hipLaunchKernelGGL((long_cols_inv<NC, TIO>), dim3(cgrid), dim3(64 * LC_WAVES), 0, s,
-                     static_cast<const uint32_t*>(work), static_cast<TIO*>(y), B, H, NR,
-                     static_cast<const h8*>(ftab));
-  return hipGetLastError();
+  for (int h0 = 0; h0 < H; h0 += chunk) {
+    const int nch = H - h0 < chunk ? H - h0 : chunk, pi0 = h0 * BP;
+    const unsigned cgrid = (unsigned)((size_t)BP * nch * (NR / LC_CBLOCK));
+    hipLaunchKernelGGL((long_cols_fwd<NC, TIO>), dim3(cgrid), dim3(64 * LC_WAVES), 0, s,
+                       static_cast<const TIO*>(u), static_cast<uint32_t*>(work), B, H, NR, pi0, inv_n,
+                       static_cast<const h8*>(ftab));
+    hipError_t err = hipGetLastError();
+    if (err != hipSuccess) return err;
+    const int nrows = nch * NC * BP;
+    hipLaunchKernelGGL((long_rows<R0, R1>), dim3(rows_grid<R0, R1>(nrows)), dim3(64 * LC_WAVES), 0, s,
+                       static_cast<uint32_t*>(work), static_cast<const float4*>(kf), nrows, BP, NC, h0, inv_n,
+                       inv_sqrt_radix<NC>(), static_cast<const h8*>(ftab), static_cast<const float4*>(tw));
+    if ((err = hipGetLastError()) != hipSuccess) return err;
+    hipLaunchKernelGGL((long_cols_inv<NC, TIO>), dim3(cgrid), dim3(64 * LC_WAVES), 0, s,
+                       static_cast<const uint32_t*>(work), static_cast<TIO*>(y), B, H, NR, pi0,
+                       static_cast<const h8*>(ftab));
+    if ((err = hipGetLastError()) != hipSuccess) return err;
+  }
+  return hipSuccess;
 }
 
 template <int NC, int R0, int R1>

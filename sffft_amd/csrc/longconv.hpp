@@ -28,7 +28,9 @@
 // twiddle applied to the result before it is stored.
 //
 // Intermediate: T and U share one workspace, [pair][k1][n2] complex fp16 (4 bytes per
-// point, 4N bytes per pair); U overwrites T row by row. Every value that enters an MFMA
+// point, 4N bytes per pair); U overwrites T row by row. The batch runs in chunks of whole
+// channels (three launches per chunk) sized by the caller's workspace: a workspace that
+// fits the Infinity Cache keeps T and U out of HBM. Every value that enters an MFMA
 // is fp16 anyway, so storing fp16 adds no rounding: with fp32 I/O the input enters
 // pass A as an fp16 value plus its fp16 remainder, and there are as many fp16
 // roundings between input and output as in a three-stage single-pass plan.
@@ -92,16 +94,19 @@ __host__ __device__ constexpr float inv_sqrt_radix() {
 }
 
 // Column-pass geometry: workgroup blockIdx.x covers LC_CBLOCK columns of pair
-// pi = h*(B/2) + bp (rows (2bp, h) and (2bp+1, h)); wavefront `wave` takes LC_COLS of them.
+// pi = pi0 + blockIdx.x / (NR / LC_CBLOCK), pi = h*(B/2) + bp (rows (2bp, h) and
+// (2bp+1, h)); wavefront `wave` takes LC_COLS of them. A launch covers the pairs of one
+// chunk of channels, from pair pi0 on; the workspace holds the chunk (slot pi - pi0).
 struct ColBlock {
-  int pi, cb;
+  int pi, slot, cb;
   size_t ra, rb;  // element offsets of the pair's two rows in u / y
 };
-__device__ __forceinline__ ColBlock col_block(int B, int H, int L, int NR, int wave) {
+__device__ __forceinline__ ColBlock col_block(int B, int H, int L, int NR, int pi0, int wave) {
   const int cblocks = NR / LC_CBLOCK;
   ColBlock c;
-  c.pi = blockIdx.x / cblocks;
-  c.cb = ((blockIdx.x - c.pi * cblocks) * LC_WAVES + wave) * LC_COLS;
+  c.slot = blockIdx.x / cblocks;
+  c.pi = pi0 + c.slot;
+  c.cb = ((blockIdx.x - c.slot * cblocks) * LC_WAVES + wave) * LC_COLS;
   const int BP = B >> 1, h = c.pi / BP, bp = c.pi - h * BP;
   c.ra = ((size_t)(2 * bp) * H + h) * L;
   c.rb = c.ra + (size_t)H * L;
@@ -114,8 +119,8 @@ __device__ __forceinline__ ColBlock col_block(int B, int H, int L, int NR, int w
 // lane, stored as 16 contiguous bytes of T.
 template <int NC, class TIO>
 __global__ void __launch_bounds__(64 * LC_WAVES)
-    long_cols_fwd(const TIO* __restrict__ u, uint32_t* __restrict__ work, int B, int H, int NR, float inv_n,
-                  const h8* __restrict__ ftab) {
+    long_cols_fwd(const TIO* __restrict__ u, uint32_t* __restrict__ work, int B, int H, int NR, int pi0,
+                  float inv_n, const h8* __restrict__ ftab) {
   constexpr int MT = LC_COLS / 16;
   constexpr int KS = NC >= 32 ? NC / 32 : 1;  // K steps over the non-zero rows
   constexpr int KT = NC / 16;                 // 16-wide tiles of k1
@@ -123,7 +128,7 @@ __global__ void __launch_bounds__(64 * LC_WAVES)
   const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int r = lane & 15, g = lane >> 4;
   const int N = NC * NR, L = N / 2;
-  const ColBlock cbk = col_block(B, H, L, NR, wave);
+  const ColBlock cbk = col_block(B, H, L, NR, pi0, wave);
   const bool live = NC >= 32 || g < 2;  // NC = 16: rows n1 >= 8 are the zero padding
 
   TIO raw[MT][KS][8];
@@ -149,7 +154,7 @@ __global__ void __launch_bounds__(64 * LC_WAVES)
         if constexpr (SPLIT) al[mt][ks][j] = (_Float16)(x - (float)hi);
       }
 
-  uint32_t* T = work + (size_t)cbk.pi * N;
+  uint32_t* T = work + (size_t)cbk.slot * N;
 #pragma unroll
   for (int kt = 0; kt < KT; kt++) {
     h8 f0[KS], f1[KS];
@@ -180,8 +185,8 @@ __global__ void __launch_bounds__(64 * LC_WAVES)
 }
 
 // ---- pass B: one row k1 of one pair per wavefront ---------------------------------
-// Row order ((h*NC + k1)*BP + bp): the B/2 rows that read one spectrum row are adjacent
-// and run in the same workgroup. The workgroup copies the DFT fragments (first kind
+// Row order ((c*NC + k1)*BP + bp) over the channels h = h0 + c of the chunk: the B/2 rows
+// that read one spectrum row are adjacent and run in the same workgroup. The workgroup copies the DFT fragments (first kind
 // only; the second is derived in registers, dft_frag<R, true>) and the row plan's
 // twiddle tables into LDS once, then its wavefronts loop over rows.
 template <int R0, int R1>
@@ -297,8 +302,8 @@ __device__ __forceinline__ void long_row(uint32_t* x, const float4* __restrict__
 
 template <int R0, int R1>
 __global__ void __launch_bounds__(64 * LC_WAVES)
-    long_rows(uint32_t* work, const float4* __restrict__ kf, int nrows, int BP, int NC, float inv_n, float sc,
-              const h8* __restrict__ ftab, const float4* __restrict__ twtab) {
+    long_rows(uint32_t* work, const float4* __restrict__ kf, int nrows, int BP, int NC, int h0, float inv_n,
+              float sc, const h8* __restrict__ ftab, const float4* __restrict__ twtab) {
   typedef WavePlan<R0, R1> P;
   typedef LongRowPlan<R0, R1> Q;
   constexpr int NR = Q::NR;
@@ -323,17 +328,18 @@ __global__ void __launch_bounds__(64 * LC_WAVES)
     // compiler-only barrier: keeps the table reads of one row from being hoisted into
     // the previous one (they would stay live across it)
     __asm__ volatile("" ::: "memory");
-    const int hk = row / BP, bp = row - hk * BP;  // hk = h*NC + k1: the spectrum row
-    const int h = hk / NC, k1 = hk - h * NC;
-    uint32_t* x = work + ((size_t)(h * BP + bp) * NC + k1) * NR;
-    long_row<R0, R1>(x, kf + (size_t)hk * (NR / 2), k1, N, inv_n, sc, F0, F1, TW1, TW2, lane);
+    const int ck = row / BP, bp = row - ck * BP;  // ck = c*NC + k1
+    const int c = ck / NC, k1 = ck - c * NC;
+    uint32_t* x = work + ((size_t)(c * BP + bp) * NC + k1) * NR;
+    const size_t hk = (size_t)(h0 + c) * NC + k1;  // the spectrum row
+    long_row<R0, R1>(x, kf + hk * (NR / 2), k1, N, inv_n, sc, F0, F1, TW1, TW2, lane);
   }
 }
 
 // ---- pass C: DFT over k1 (all NC rows of U), outputs n1 < NC/2 ---------------------
 template <int NC, class TIO>
 __global__ void __launch_bounds__(64 * LC_WAVES)
-    long_cols_inv(const uint32_t* __restrict__ work, TIO* __restrict__ y, int B, int H, int NR,
+    long_cols_inv(const uint32_t* __restrict__ work, TIO* __restrict__ y, int B, int H, int NR, int pi0,
                   const h8* __restrict__ ftab) {
   constexpr int MT = LC_COLS / 16;
   constexpr int KS = NC / 16;                 // K steps over all k1
@@ -341,8 +347,8 @@ __global__ void __launch_bounds__(64 * LC_WAVES)
   const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int r = lane & 15, g = lane >> 4;
   const int N = NC * NR, L = N / 2;
-  const ColBlock cbk = col_block(B, H, L, NR, wave);
-  const uint32_t* U = work + (size_t)cbk.pi * N;
+  const ColBlock cbk = col_block(B, H, L, NR, pi0, wave);
+  const uint32_t* U = work + (size_t)cbk.slot * N;
 
   uint32_t raw[MT][KS][4];
 #pragma unroll

@@ -34,7 +34,8 @@ const Entry* entries_L16384(int* n);
 
 // Multi-pass plans (mode 2, longconv.hpp): column radix nc, row plan r0 x r1; the three
 // passes run on one stream with the caller's workspace.
-typedef hipError_t (*long_launch_fn)(const void* u, const void* kf, void* y, void* work, int B, int H,
+// `chunk` channels per group of three launches (the workspace holds chunk*B/2 pairs).
+typedef hipError_t (*long_launch_fn)(const void* u, const void* kf, void* y, void* work, int B, int H, int chunk,
                                      const void* ftab, const void* tw, hipStream_t stream);
 struct LongEntry {
   int nc, r0, r1, lds_bytes;  // lds_bytes: the row pass's tables

@@ -95,7 +95,9 @@ def test_long_plans_registry():
         NR = p.r1 * p.r2
         frags = ((p.r1 // 16) ** 2 + (0 if p.r1 == p.r2 else (p.r2 // 16) ** 2)) * 64 * 16
         assert sf.lds_bytes(L, p) == frags + (1 if p.r1 == p.r2 else 2) * NR * 8
-        assert sf.work_bytes(8, 768, L, p) == 4 * 768 * 2 * L * 4
+        per_channel = 4 * 2 * L * 4  # B/2 pairs of 2L complex fp16 points
+        assert sf.work_bytes(8, 768, L, p) == min(768, (96 << 20) // per_channel) * per_channel
+        assert sf.work_bytes(8, 3, L, p) == min(3, (96 << 20) // per_channel) * per_channel
     for L in sf.LONG_LENGTHS:
         listed = sf.plans(L)
         assert listed and all(q.mode == 2 and q.r0 * q.r1 * q.r2 == 2 * L for q in listed)
@@ -125,11 +127,12 @@ def test_long_conv_argument_errors_need_no_gpu():
     null = ctypes.c_void_p(0)
     L, B, H = 65536, 8, 4
     need = sf.work_bytes(B, H, L, p)
+    assert need == H * (B // 2) * 2 * L * 4  # four channels fit one 96 MiB chunk
     io = B * H * L * 4
     u, kf, y, w = (ctypes.c_void_p((1 << 40) + i * (1 << 34)) for i in range(4))
     f = lib.sffft_conv_long_f32
     assert f(u, kf, y, null, need, B, H, L, ctypes.byref(p), null) == sf.SFFFT_EINVAL          # no workspace
-    assert f(u, kf, y, w, need - 1, B, H, L, ctypes.byref(p), null) == sf.SFFFT_EINVAL         # too small
+    assert f(u, kf, y, w, need // H - 1, B, H, L, ctypes.byref(p), null) == sf.SFFFT_EINVAL    # < one channel
     assert f(u, kf, y, w, need, 7, H, L, ctypes.byref(p), null) == sf.SFFFT_EINVAL            # B odd
     assert f(u, kf, y, ctypes.c_void_p((1 << 40) + 8), need, B, H, L, ctypes.byref(p),
              null) == sf.SFFFT_EINVAL                                                         # misaligned

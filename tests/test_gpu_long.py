@@ -95,6 +95,23 @@ def test_long_workspace_reuse_and_delta(dev):
     assert oracle.rel_l2(y1, exp) <= 5e-4
 
 
+def test_long_chunks_agree(dev):
+    """The batch runs in chunks of whole channels sized by the workspace: one channel per
+    chunk, a ragged last chunk (2 of 5 channels) and the whole batch give the same bits."""
+    import torch
+
+    L, B, H = 32768, 4, 5
+    plan = sf.long_plan("32x64x32")
+    u, k = oracle.gen_inputs(B, H, L, seed=21)
+    per = (B // 2) * 2 * L * 4
+    outs = []
+    for nch in (1, 3, H):
+        work = torch.empty(nch * per + 8, dtype=torch.uint8, device=dev)  # a few spare bytes are ignored
+        outs.append(_run(dev, u, k, plan, "fp32", work=work))
+    assert np.array_equal(outs[0], outs[1]) and np.array_equal(outs[0], outs[2])
+    assert oracle.rel_l2(outs[0], oracle.conv(u, k)) <= 5e-4
+
+
 def test_long_full_batch_properties(dev):
     """B=8, H=768, L=32768 fp32 with the default plan: sampled sequences against the
     oracle; swapping two batch pairs permutes the output bit for bit; two launches
