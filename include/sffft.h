@@ -124,6 +124,20 @@ int sffft_conv_long_f32(const float* u, const void* kf, float* y, void* work, si
 int sffft_conv_long_bf16(const uint16_t* u, const void* kf, uint16_t* y, void* work, size_t work_bytes, int B, int H,
                          int L, const sffft_plan* plan, void* stream);
 
+/* Circular (non-causal) convolution of period N with a multi-pass plan (r0*r1*r2 = N):
+ *   y[b,h,n] = sum_{m<N} u[b,h,m] * k[h,(n-m) mod N],  n < N,
+ * u, y [B][H][N], k [H][N]. The reference lists non-causal and circular convolution as not
+ * exposed (README.md:174); no counterpart. The same passes as sffft_conv_long_* over rows of
+ * length N with no zero half; the spectrum is the DFT of the unpadded filter
+ * (sffft_spectrum_circular, same order as sffft_spectrum for the plan, H*N*8 bytes, `work`
+ * as in sffft_spectrum). Workspace: sffft_work_bytes(B, H, N/2, plan) (same chunking). */
+int sffft_spectrum_circular(const float* k, int H, int N, const sffft_plan* plan, void* kf, void* work,
+                            void* stream);
+int sffft_circconv_long_f32(const float* u, const void* kf, float* y, void* work, size_t work_bytes, int B, int H,
+                            int N, const sffft_plan* plan, void* stream);
+int sffft_circconv_long_bf16(const uint16_t* u, const void* kf, uint16_t* y, void* work, size_t work_bytes, int B,
+                             int H, int N, const sffft_plan* plan, void* stream);
+
 /* fp32 -> bf16 (round to nearest even) on the device. Replaces tobf16 (src/sffft.cu:306). */
 int sffft_to_bf16(const float* x, uint16_t* y, size_t n, void* stream);
 

@@ -95,6 +95,16 @@ def conv(u, k):
     return direct_conv(u, k) if u.shape[-1] <= 2048 else fft_conv(u, k)
 
 
+def circ_conv(u, k):
+    """fp64 circular convolution of period N over the last axis, y[..., n] = sum_m u[..., m]
+    k[..., (n - m) mod N], via numpy's FFT. The reference has no circular convolution
+    (README.md:174); this checker is pinned against the brute-force sum in
+    tests/test_oracle.py."""
+    u = np.asarray(u, np.float64)
+    k = np.asarray(k, np.float64)
+    return np.fft.ifft(np.fft.fft(u, axis=-1) * np.fft.fft(k, axis=-1), axis=-1).real
+
+
 def spectrum_p_order(k_row, r0, r1, r2=1):
     """Unnormalised spectrum of one zero-padded filter row in the reference digit order
     (src/sffft.cu:283-288): complex128 array of length 2L."""

@@ -107,6 +107,9 @@ def lib() -> ctypes.CDLL:
             "sffft_work_bytes": (sz, [ci, ci, ci, P]),
             "sffft_conv_long_f32": (ci, [vp, vp, vp, vp, sz, ci, ci, ci, P, vp]),
             "sffft_conv_long_bf16": (ci, [vp, vp, vp, vp, sz, ci, ci, ci, P, vp]),
+            "sffft_spectrum_circular": (ci, [vp, ci, ci, P, vp, vp, vp]),
+            "sffft_circconv_long_f32": (ci, [vp, vp, vp, vp, sz, ci, ci, ci, P, vp]),
+            "sffft_circconv_long_bf16": (ci, [vp, vp, vp, vp, sz, ci, ci, ci, P, vp]),
             "sffft_to_bf16": (ci, [vp, vp, sz, vp]),
             "sffft_dispatch_floor": (ci, [ci, ci, ci, P, vp]),
             "sffft_dft_table": (ci, [vp, sz]),
@@ -301,6 +304,45 @@ def conv_long(u, kf, plan: Plan, out=None, work=None):
     wb = work.numel() * work.element_size()
     _check(fn(_ptr(u), _ptr(kf), _ptr(y), _ptr(work), wb, B, H, L, ctypes.byref(plan), _stream()),
            "sffft_conv_long")
+    return y
+
+
+def spectrum_circular(k, plan: Plan, work=None):
+    """Spectrum [H, N] complex64 of the unpadded filters k [H, N] (fp32, cuda) for a circular
+    convolution of period N = r0*r1*r2 with a multi-pass plan."""
+    import torch
+
+    assert k.is_cuda and k.dtype == torch.float32 and k.dim() == 2
+    k = k.contiguous()
+    H, N = k.shape
+    kf = torch.empty((H, N), dtype=torch.complex64, device=k.device)
+    if work is None:
+        work = torch.empty_like(kf)
+    _check(lib().sffft_spectrum_circular(_ptr(k), H, N, ctypes.byref(plan), _ptr(kf), _ptr(work), _stream()),
+           "sffft_spectrum_circular")
+    return kf
+
+
+def circconv(u, kf, plan: Plan, out=None, work=None):
+    """y[b,h,n] = sum_m u[b,h,m] k[h,(n-m) mod N] for u [B, H, N] fp32 or bf16 (cuda), kf from
+    spectrum_circular(); a multi-pass plan, B even."""
+    import torch
+
+    u = u.contiguous()
+    B, H, N = u.shape
+    y = torch.empty_like(u) if out is None else out
+    nbytes = work_bytes(B, H, N // 2, plan)
+    if work is None:
+        work = torch.empty(max(nbytes, 16), dtype=torch.uint8, device=u.device)
+    if u.dtype == torch.float32:
+        fn = lib().sffft_circconv_long_f32
+    elif u.dtype == torch.bfloat16:
+        fn = lib().sffft_circconv_long_bf16
+    else:
+        raise TypeError(f"unsupported dtype {u.dtype}")
+    wb = work.numel() * work.element_size()
+    _check(fn(_ptr(u), _ptr(kf), _ptr(y), _ptr(work), wb, B, H, N, ctypes.byref(plan), _stream()),
+           "sffft_circconv_long")
     return y
 
 

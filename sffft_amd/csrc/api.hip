@@ -287,8 +287,9 @@ __device__ inline void kernel_order_digits_rt(int idx, int r0, int r1, int r2, i
 // One in-place decimation-in-frequency stage over digit J (Appendix-A order of the
 // reference: after all stages position p = d0*(R1 R2) + d1*R2 + d2 holds
 // DFT_N(pad(k))[d0 + R0 d1 + R0 R1 d2]). One thread per line of R_J points; fp64
-// arithmetic, fp32 storage. Stage 0 reads the real filter rows zero-padded to N.
-__global__ void spectrum_stage_kernel(const float* __restrict__ k, float2* work, int H, int L, int r0, int r1,
+// arithmetic, fp32 storage. Stage 0 reads the real filter rows of length klen (L, or N for
+// a circular convolution), zero-padded to N.
+__global__ void spectrum_stage_kernel(const float* __restrict__ k, float2* work, int H, int klen, int r0, int r1,
                                       int r2, int J) {
   __shared__ double wc[64], ws[64];
   const int N = r0 * r1 * r2, S = r2 > 1 ? 3 : 2;
@@ -312,7 +313,7 @@ __global__ void spectrum_stage_kernel(const float* __restrict__ k, float2* work,
   for (int t = 0; t < R; t++) {
     const int p = base + t * sJ;
     if (J == 0)
-      x[t] = make_float2(p < L ? k[(size_t)h * L + p] : 0.f, 0.f);
+      x[t] = make_float2(p < klen ? k[(size_t)h * klen + p] : 0.f, 0.f);
     else
       x[t] = row[p];
   }
@@ -413,9 +414,10 @@ size_t work_bytes(int B, int H, int L) {
   return ch * per;
 }
 
+// circ: circular convolution of period 2L (rows of length 2L)
 template <int IO>
 int conv_long(const void* u, const void* kf, void* y, void* work, size_t wbytes, int B, int H, int L,
-              const sffft_plan* p, void* stream) {
+              const sffft_plan* p, void* stream, int circ = 0) {
   if (!u || !kf || !y || !work || B < 2 || H < 1 || (long long)B * H > INT_MAX) return SFFFT_EINVAL;
   int rc = check_shape(L, p);
   if (rc) return rc;
@@ -432,7 +434,7 @@ int conv_long(const void* u, const void* kf, void* y, void* work, size_t wbytes,
     const uintptr_t x = (uintptr_t)a, z = (uintptr_t)b;
     return x < z + nb && z < x + na;
   };
-  const size_t io_bytes = (size_t)B * H * L * (IO ? 2 : 4);
+  const size_t io_bytes = (size_t)B * H * L * (circ ? 2 : 1) * (IO ? 2 : 4);
   wbytes = (size_t)chunk * channel_work_bytes(B, L);  // the part the passes use
   if (overlaps(work, wbytes, u, io_bytes) || overlaps(work, wbytes, y, io_bytes) ||
       overlaps(work, wbytes, kf, (size_t)H * 2 * L * 8))
@@ -443,7 +445,7 @@ int conv_long(const void* u, const void* kf, void* y, void* work, size_t wbytes,
   if ((rc = device_table(&table))) return rc;
   const void* tw = nullptr;
   if ((rc = device_twiddles(p->r1, p->r2, &tw))) return rc;
-  return hip_status(e->launch[IO](u, kf, y, work, B, H, chunk, table, tw, (hipStream_t)stream),
+  return hip_status(e->launch[circ][IO](u, kf, y, work, B, H, chunk, table, tw, (hipStream_t)stream),
                     "multi-pass launch");
 }
 
@@ -459,6 +461,28 @@ int long_plans_for(int L, const LongEntry** out, int cap) {
   return k;
 }
 
+int spectrum_impl(const float* k, int H, int L, int klen, const sffft_plan* plan, void* kf, void* work,
+                  void* stream) {
+  if (!k || !kf || !work || H < 1 || kf == work) return SFFFT_EINVAL;
+  const int rc = check_shape(L, plan);
+  if (rc) return rc;
+  const int N = 2 * L, S = plan->r2 > 1 ? 3 : 2;
+  hipStream_t s = (hipStream_t)stream;
+  float2* w = static_cast<float2*>(work);
+  for (int J = 0; J < S; J++) {
+    const int R = J == 0 ? plan->r0 : J == 1 ? plan->r1 : plan->r2;
+    const size_t threads = (size_t)H * (N / R);
+    hipLaunchKernelGGL(spectrum_stage_kernel, dim3((unsigned)((threads + 127) / 128)), dim3(128), 0, s, k, w, H,
+                       klen, plan->r0, plan->r1, plan->r2, J);
+    const int st = hip_status(hipGetLastError(), "spectrum stage launch");
+    if (st) return st;
+  }
+  const size_t total = (size_t)H * N;
+  hipLaunchKernelGGL(spectrum_permute_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s,
+                     (const float2*)w, static_cast<float2*>(kf), H, plan->r0, plan->r1, plan->r2, plan->mode, 0,
+                     last_stage_scale(plan));
+  return hip_status(hipGetLastError(), "spectrum permute launch");
+}
 }  // namespace
 }  // namespace sffft
 
@@ -538,25 +562,25 @@ size_t sffft_spectrum_bytes(int H, int L) {
 }
 
 int sffft_spectrum(const float* k, int H, int L, const sffft_plan* plan, void* kf, void* work, void* stream) {
-  if (!k || !kf || !work || H < 1 || kf == work) return SFFFT_EINVAL;
-  const int rc = check_shape(L, plan);
-  if (rc) return rc;
-  const int N = 2 * L, S = plan->r2 > 1 ? 3 : 2;
-  hipStream_t s = (hipStream_t)stream;
-  float2* w = static_cast<float2*>(work);
-  for (int J = 0; J < S; J++) {
-    const int R = J == 0 ? plan->r0 : J == 1 ? plan->r1 : plan->r2;
-    const size_t threads = (size_t)H * (N / R);
-    hipLaunchKernelGGL(spectrum_stage_kernel, dim3((unsigned)((threads + 127) / 128)), dim3(128), 0, s, k, w, H, L,
-                       plan->r0, plan->r1, plan->r2, J);
-    const int st = hip_status(hipGetLastError(), "spectrum stage launch");
-    if (st) return st;
-  }
-  const size_t total = (size_t)H * N;
-  hipLaunchKernelGGL(spectrum_permute_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s,
-                     (const float2*)w, static_cast<float2*>(kf), H, plan->r0, plan->r1, plan->r2, plan->mode, 0,
-                     last_stage_scale(plan));
-  return hip_status(hipGetLastError(), "spectrum permute launch");
+  return spectrum_impl(k, H, L, L, plan, kf, work, stream);
+}
+
+int sffft_spectrum_circular(const float* k, int H, int N, const sffft_plan* plan, void* kf, void* work,
+                            void* stream) {
+  if (N < 2 || N % 2 || !plan || plan->mode != 2) return SFFFT_EINVAL;
+  return spectrum_impl(k, H, N / 2, N, plan, kf, work, stream);
+}
+
+int sffft_circconv_long_f32(const float* u, const void* kf, float* y, void* work, size_t work_bytes, int B, int H,
+                            int N, const sffft_plan* plan, void* stream) {
+  if (N < 2 || N % 2) return SFFFT_EINVAL;
+  return conv_long<0>(u, kf, y, work, work_bytes, B, H, N / 2, plan, stream, 1);
+}
+
+int sffft_circconv_long_bf16(const uint16_t* u, const void* kf, uint16_t* y, void* work, size_t work_bytes, int B,
+                             int H, int N, const sffft_plan* plan, void* stream) {
+  if (N < 2 || N % 2) return SFFFT_EINVAL;
+  return conv_long<1>(u, kf, y, work, work_bytes, B, H, N / 2, plan, stream, 1);
 }
 
 int sffft_spectrum_from_natural(const void* kc, int H, int L, const sffft_plan* plan, void* kf, void* stream) {

@@ -36,8 +36,8 @@ static unsigned rows_grid(int nrows) {
 }
 
 // The three passes on one stream, for chunks of `chunk` channels: the workspace holds
-// chunk*(B/2) pairs of N complex fp16 points.
-template <int NC, int R0, int R1, class TIO>
+// chunk*(B/2) pairs of N complex fp16 points. CIRC: circular convolution of period N.
+template <int NC, int R0, int R1, class TIO, bool CIRC>
 static hipError_t launch_long(const void* u, const void* kf, void* y, void* work, int B, int H, int chunk,
                               const void* ftab, const void* tw, hipStream_t s) {
   constexpr int NR = R0 * R1, N = NC * NR;
@@ -46,7 +46,7 @@ static hipError_t launch_long(const void* u, const void* kf, void* y, void* work
   for (int h0 = 0; h0 < H; h0 += chunk) {
     const int nch = H - h0 < chunk ? H - h0 : chunk, pi0 = h0 * BP;
     const unsigned cgrid = (unsigned)((size_t)BP * nch * (NR / LC_CBLOCK));
-    hipLaunchKernelGGL((long_cols_fwd<NC, TIO>), dim3(cgrid), dim3(64 * LC_WAVES), 0, s,
+    hipLaunchKernelGGL((long_cols_fwd<NC, TIO, CIRC>), dim3(cgrid), dim3(64 * LC_WAVES), 0, s,
                        static_cast<const TIO*>(u), static_cast<uint32_t*>(work), B, H, NR, pi0, inv_n,
                        static_cast<const h8*>(ftab));
     hipError_t err = hipGetLastError();
@@ -56,7 +56,7 @@ static hipError_t launch_long(const void* u, const void* kf, void* y, void* work
                        static_cast<uint32_t*>(work), static_cast<const float4*>(kf), nrows, BP, NC, h0, inv_n,
                        inv_sqrt_radix<NC>(), static_cast<const h8*>(ftab), static_cast<const float4*>(tw));
     if ((err = hipGetLastError()) != hipSuccess) return err;
-    hipLaunchKernelGGL((long_cols_inv<NC, TIO>), dim3(cgrid), dim3(64 * LC_WAVES), 0, s,
+    hipLaunchKernelGGL((long_cols_inv<NC, TIO, CIRC>), dim3(cgrid), dim3(64 * LC_WAVES), 0, s,
                        static_cast<const uint32_t*>(work), static_cast<TIO*>(y), B, H, NR, pi0,
                        static_cast<const h8*>(ftab));
     if ((err = hipGetLastError()) != hipSuccess) return err;
@@ -67,7 +67,8 @@ static hipError_t launch_long(const void* u, const void* kf, void* y, void* work
 template <int NC, int R0, int R1>
 static LongEntry make_long_entry() {
   LongEntry e = {NC, R0, R1, LongRowPlan<R0, R1>::LDS_BYTES,
-                 {&launch_long<NC, R0, R1, float>, &launch_long<NC, R0, R1, uint16_t>},
+                 {{&launch_long<NC, R0, R1, float, false>, &launch_long<NC, R0, R1, uint16_t, false>},
+                  {&launch_long<NC, R0, R1, float, true>, &launch_long<NC, R0, R1, uint16_t, true>}},
                  reinterpret_cast<const void*>(&long_rows<R0, R1>)};
   return e;
 }

@@ -35,6 +35,10 @@
 // pass A as an fp16 value plus its fp16 remainder, and there are as many fp16
 // roundings between input and output as in a three-stage single-pass plan.
 //
+// Circular convolution of period N (CIRC): y[n] = sum_{m<N} x[m] k[(n - m) mod N], rows of
+// length N. The same passes, with pass A contracting over all NC rows and pass C storing
+// all of them; the spectrum is the DFT of the unpadded length-N filter.
+//
 // HBM traffic per pair: pass A reads the two input rows and writes T (4N), pass B reads
 // and rewrites it (8N) and its channel's spectrum (8N per channel, shared by the B/2
 // pairs through L2), pass C reads U (4N) and writes the two output rows.
@@ -113,23 +117,23 @@ __device__ __forceinline__ ColBlock col_block(int B, int H, int L, int NR, int p
   return c;
 }
 
-// ---- pass A: DFT over n1 (rows n1 < NC/2 only), N-level twiddle, T in fp16 ----------
-// Lane (r, g) of tile (mt, ks) holds x[n1 = 16ks + 4g + j][n2 = cb + 16mt + r] (slots j: row
-// a, 4 + j: row b); the result tile D[m][k1] puts four consecutive columns of one k1 in a
-// lane, stored as 16 contiguous bytes of T.
-template <int NC, class TIO>
+// ---- pass A: DFT over n1 (rows n1 < NC/2 only, or all with CIRC), N-level twiddle,
+// T in fp16. Lane (r, g) of tile (mt, ks) holds x[n1 = 16ks + 4g + j][n2 = cb + 16mt + r]
+// (slots j: row a, 4 + j: row b); the result tile D[m][k1] puts four consecutive columns
+// of one k1 in a lane, stored as 16 contiguous bytes of T.
+template <int NC, class TIO, bool CIRC>
 __global__ void __launch_bounds__(64 * LC_WAVES)
     long_cols_fwd(const TIO* __restrict__ u, uint32_t* __restrict__ work, int B, int H, int NR, int pi0,
                   float inv_n, const h8* __restrict__ ftab) {
   constexpr int MT = LC_COLS / 16;
-  constexpr int KS = NC >= 32 ? NC / 32 : 1;  // K steps over the non-zero rows
-  constexpr int KT = NC / 16;                 // 16-wide tiles of k1
-  constexpr bool SPLIT = sizeof(TIO) == 4;    // fp32 input as fp16 value + fp16 remainder
+  constexpr int KS = CIRC ? NC / 16 : NC >= 32 ? NC / 32 : 1;  // K steps over the non-zero rows
+  constexpr int KT = NC / 16;                                  // 16-wide tiles of k1
+  constexpr bool SPLIT = sizeof(TIO) == 4;  // fp32 input as fp16 value + fp16 remainder
   const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int r = lane & 15, g = lane >> 4;
-  const int N = NC * NR, L = N / 2;
-  const ColBlock cbk = col_block(B, H, L, NR, pi0, wave);
-  const bool live = NC >= 32 || g < 2;  // NC = 16: rows n1 >= 8 are the zero padding
+  const int N = NC * NR, LEN = CIRC ? N : N / 2;  // row length of u and y
+  const ColBlock cbk = col_block(B, H, LEN, NR, pi0, wave);
+  const bool live = CIRC || NC >= 32 || g < 2;  // NC = 16: rows n1 >= 8 are the zero padding
 
   TIO raw[MT][KS][8];
 #pragma unroll
@@ -336,18 +340,18 @@ __global__ void __launch_bounds__(64 * LC_WAVES)
   }
 }
 
-// ---- pass C: DFT over k1 (all NC rows of U), outputs n1 < NC/2 ---------------------
-template <int NC, class TIO>
+// ---- pass C: DFT over k1 (all NC rows of U), outputs n1 < NC/2 (all with CIRC) --------
+template <int NC, class TIO, bool CIRC>
 __global__ void __launch_bounds__(64 * LC_WAVES)
     long_cols_inv(const uint32_t* __restrict__ work, TIO* __restrict__ y, int B, int H, int NR, int pi0,
                   const h8* __restrict__ ftab) {
   constexpr int MT = LC_COLS / 16;
-  constexpr int KS = NC / 16;                 // K steps over all k1
-  constexpr int NT = NC >= 32 ? NC / 32 : 1;  // result tiles of n1 < NC/2
+  constexpr int KS = NC / 16;                                  // K steps over all k1
+  constexpr int NT = CIRC ? NC / 16 : NC >= 32 ? NC / 32 : 1;  // result tiles of the stored n1
   const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int r = lane & 15, g = lane >> 4;
-  const int N = NC * NR, L = N / 2;
-  const ColBlock cbk = col_block(B, H, L, NR, pi0, wave);
+  const int N = NC * NR, LEN = CIRC ? N : N / 2;
+  const ColBlock cbk = col_block(B, H, LEN, NR, pi0, wave);
   const uint32_t* U = work + (size_t)cbk.slot * N;
 
   uint32_t raw[MT][KS][4];
@@ -373,7 +377,7 @@ __global__ void __launch_bounds__(64 * LC_WAVES)
       f1[ks] = cf_frag<NC, true>(ftab, nu, ks, 1, lane);
     }
     const int n1 = 16 * nu + r;
-    const bool out = NC >= 32 || n1 < NC / 2;
+    const bool out = CIRC || NC >= 32 || n1 < NC / 2;
 #pragma unroll
     for (int mt = 0; mt < MT; mt++) {
       f4 dr = {0.f, 0.f, 0.f, 0.f}, di = {0.f, 0.f, 0.f, 0.f};

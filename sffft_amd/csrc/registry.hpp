@@ -39,7 +39,7 @@ typedef hipError_t (*long_launch_fn)(const void* u, const void* kf, void* y, voi
                                      const void* ftab, const void* tw, hipStream_t stream);
 struct LongEntry {
   int nc, r0, r1, lds_bytes;  // lds_bytes: the row pass's tables
-  long_launch_fn launch[2];   // [io: 0 = fp32, 1 = bf16]
+  long_launch_fn launch[2][2];  // [0 = causal, 1 = circular of period 2L][io: 0 = fp32, 1 = bf16]
   const void* rows_func;      // the row-pass kernel (occupancy queries)
 };
 // Defined by long_inst.hip.

@@ -31,7 +31,7 @@ from typing import List, Optional, Sequence
 
 import torch
 
-from . import Plan, conv as _conv, default_plan, spectrum as _spectrum
+from . import LONG_DEFAULT_PLANS, Plan, conv as _conv, default_plan, spectrum as _spectrum
 
 PLAN_FIELDS = ("r0", "r1", "r2", "waves", "acc", "cached", "seqs", "mode", "channels")
 
@@ -108,14 +108,19 @@ def filter_grad(u: torch.Tensor, dy: torch.Tensor) -> torch.Tensor:
     """dk[h, j] = sum_b sum_{n >= j} dy[b, h, n] u[b, h, n - j] for u, dy [B, H, L] (fp32 [H, L]).
 
     Computed on the GPU kernels as flip(causal_conv(flip(dy), u)) per sequence, summed over b:
-    the B*H rows of u are the filters (fp32 spectra) of a batch-of-one convolution.
+    the B*H rows of u are the filters (fp32 spectra) of a batch-of-one convolution. Multi-pass
+    lengths (L > 16384) take pairs of sequences only, so there each row of flip(dy) is paired
+    with a zero row (a batch of two whose second row is discarded).
     """
     B, H, L = u.shape
-    plan = default_plan(L, "fp32", 1)  # one sequence per transform: batch of one
+    pairs_only = L in LONG_DEFAULT_PLANS
+    plan = default_plan(L, "fp32", 2 if pairs_only else 1)  # one sequence per transform: batch of one
     fields = plan_fields(plan)
     kf = torch.ops.sffft.spectrum(u.detach().float().reshape(B * H, L).contiguous(), fields)
-    w = dy.float().flip(-1).reshape(1, B * H, L).contiguous()
-    r = torch.ops.sffft.conv(w, kf, fields)
+    w = dy.float().flip(-1).reshape(1, B * H, L)
+    if pairs_only:
+        w = torch.cat([w, torch.zeros_like(w)])
+    r = torch.ops.sffft.conv(w.contiguous(), kf, fields)[:1]
     return r.reshape(B, H, L).flip(-1).sum(0)
 
 

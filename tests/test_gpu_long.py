@@ -141,3 +141,40 @@ def test_long_full_batch_properties(dev):
         err = oracle.rel_l2(y[b, hs].cpu().numpy()[None], ref)
         print(f"  b={b} sampled rel_l2={err:.3e}", flush=True)
         assert err <= 5e-4
+
+
+@pytest.mark.parametrize("N,spec", [(8192, "32x16x16"), (65536, "64x32x32"), (131072, "32x64x64")])
+def test_circular_conv_matches_oracle(dev, N, spec):
+    """Circular convolution of period N (sffft_circconv_long_*): every output against the fp64
+    circular convolution, both I/O types; with a zero second half of u and a zero-padded filter
+    it equals the causal convolution.
+
+    fp32 bound 6e-4: with no zero half in the transform input, each fp16 rounding carries about
+    twice the noise energy per unit of output signal of the causal case (4.2e-4 there, so about
+    sqrt(2) x 4.2e-4 here), with the same arithmetic."""
+    import torch
+
+    plan = sf.long_plan(spec)
+    B, H = 4, 3
+    rng = np.random.default_rng(N)
+    u = rng.standard_normal((B, H, N)).astype(np.float32)
+    k = (rng.standard_normal((H, N)) * np.exp(-np.arange(N) / (N / 8)) / np.sqrt(N)).astype(np.float32)
+    ref = oracle.circ_conv(u, k[None])
+    kf = sf.spectrum_circular(torch.from_numpy(k).to(dev), plan)
+    for io in ("fp32", "bf16"):
+        ud = torch.from_numpy(u).to(dev)
+        if io == "bf16":
+            ud = sf.to_bf16(ud)
+        y = sf.circconv(ud, kf, plan).float().cpu().numpy()
+        err = oracle.rel_l2(y, ref)
+        print(f"case circular N={N} {spec} io={io} rel_l2={err:.3e}", flush=True)
+        assert np.isfinite(err) and err <= (6e-4 if io == "fp32" else BOUND[io]), (N, spec, io, err)
+    L = N // 2
+    uc = u.copy()
+    uc[..., L:] = 0
+    kc = k.copy()
+    kc[:, L:] = 0
+    kfc = sf.spectrum_circular(torch.from_numpy(kc).to(dev), plan)
+    y = sf.circconv(torch.from_numpy(uc).to(dev), kfc, plan).cpu().numpy()
+    ref_causal = oracle.conv(uc[..., :L].copy(), kc[:, :L].copy())
+    assert oracle.rel_l2(y[..., :L], ref_causal) <= 5e-4

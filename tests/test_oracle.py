@@ -167,3 +167,20 @@ def test_golden_vectors():
     u, k = oracle.ref_inputs(1, 1, 128)
     assert np.array_equal(u, g["ref_u"]) and np.array_equal(k, g["ref_k"])
     assert np.allclose(_np_causal(g["ref_u"], g["ref_k"]), g["ref_y"], rtol=0, atol=1e-12)
+
+
+def test_circ_conv_against_brute_force():
+    # the checker of the circular-convolution entry points: numpy FFT in fp64 against the
+    # defining sum, and a planted index mistake (n + m instead of n - m) fails it
+    rng = np.random.default_rng(4)
+    N = 48
+    u, k = rng.standard_normal((3, N)), rng.standard_normal((3, N))
+    brute = np.array([[sum(u[r, m] * k[r, (n - m) % N] for m in range(N)) for n in range(N)] for r in range(3)])
+    assert np.abs(oracle.circ_conv(u, k) - brute).max() < 1e-12
+    wrong = np.array([[sum(u[r, m] * k[r, (n + m) % N] for m in range(N)) for n in range(N)] for r in range(3)])
+    assert np.abs(oracle.circ_conv(u, k) - wrong).max() > 1e-3
+    # period N with the second half of u zero and k zero-padded is the causal convolution
+    L = 32
+    u2, k2 = rng.standard_normal(L), rng.standard_normal(L)
+    pad = lambda x: np.concatenate([x, np.zeros(L)])
+    assert np.abs(oracle.circ_conv(pad(u2), pad(k2))[:L] - np.convolve(u2, k2)[:L]).max() < 1e-12

@@ -32,10 +32,14 @@ def test_fake_shapes():
         assert y.shape == (8, 768, 1024) and y.dtype == torch.bfloat16
 
 
-@pytest.mark.parametrize("L", sf.LENGTHS)
+@pytest.mark.parametrize("L", sf.LENGTHS + sf.LONG_LENGTHS)
 def test_default_plans_are_compiled(L):
     for io in ("fp32", "bf16"):
         for B in (8, 7):
+            if L in sf.LONG_LENGTHS and B % 2:
+                with pytest.raises(ValueError):  # multi-pass plans take pairs of sequences
+                    sf.default_plan(L, io, B)
+                continue
             p = sf.default_plan(L, io, B)
             assert sf.plan_check(L, p) == 0, (L, io, B, p)
             assert B % p.seqs == 0
@@ -112,9 +116,9 @@ def test_opcheck(dev):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("L", [512, 4096])
+@pytest.mark.parametrize("L", [512, 4096, 32768])
 def test_input_gradient(dev, L):
-    B, H = 4, 5
+    B, H = (4, 5) if L <= 16384 else (2, 3)
     u, k, _, k_np = _inputs(dev, B, H, L, seed=11)
     w = torch.randn(B, H, L, device=dev, generator=torch.Generator(device=dev).manual_seed(2))
     lc = torch_ops.LongConv()
@@ -129,9 +133,9 @@ def test_input_gradient(dev, L):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("L,io", [(512, "fp32"), (4096, "fp32"), (1024, "bf16")])
+@pytest.mark.parametrize("L,io", [(512, "fp32"), (4096, "fp32"), (1024, "bf16"), (32768, "fp32")])
 def test_filter_gradient(dev, L, io):
-    B, H = 4, 5
+    B, H = (4, 5) if L <= 16384 else (2, 3)
     u, k, u_np, k_np = _inputs(dev, B, H, L, seed=13)
     if io == "bf16":
         u = u.to(torch.bfloat16)
