@@ -91,6 +91,16 @@ size_t sffft_spectrum_bytes(int H, int L);
  * Arithmetic: fp64 accumulation and twiddles, fp32 storage between the stages. */
 int sffft_spectrum(const float* k, int H, int L, const sffft_plan* plan, void* kf, void* work, void* stream);
 
+/* Complex input: the spectrum of the complex filter kr + i*ki (kr, ki [H][L] fp32) for a plan
+ * with two sequences per transform (seqs = 2; every mode-1 and mode-2 plan). With it,
+ * sffft_conv_* and sffft_conv_long_* compute the complex causal convolution
+ *   y[b] + i y[b+1] = sum_{m<=n} (u[b,m] + i u[b+1,m]) (kr[n-m] + i ki[n-m])
+ * for every even b: batch rows 2b' and 2b'+1 of u and y are the real and imaginary planes of
+ * complex sequence b'. The reference takes real input only (README.md:174); no counterpart.
+ * `work` as in sffft_spectrum; kf holds the sum of both spectra. */
+int sffft_spectrum_complex(const float* kr, const float* ki, int H, int L, const sffft_plan* plan, void* kf,
+                           void* work, void* stream);
+
 /* Same, from an unnormalised natural-order spectrum kc [H][2L] complex64
  * (kc[h][f] = sum_n k[h][n] exp(-2 pi i f n / 2L), e.g. from hipFFT C2C).
  * Replaces permuteK (src/sffft.cu:283-288). kc and kf must not overlap. */

@@ -108,6 +108,7 @@ def lib() -> ctypes.CDLL:
             "sffft_conv_long_f32": (ci, [vp, vp, vp, vp, sz, ci, ci, ci, P, vp]),
             "sffft_conv_long_bf16": (ci, [vp, vp, vp, vp, sz, ci, ci, ci, P, vp]),
             "sffft_spectrum_circular": (ci, [vp, ci, ci, P, vp, vp, vp]),
+            "sffft_spectrum_complex": (ci, [vp, vp, ci, ci, P, vp, vp, vp]),
             "sffft_circconv_long_f32": (ci, [vp, vp, vp, vp, sz, ci, ci, ci, P, vp]),
             "sffft_circconv_long_bf16": (ci, [vp, vp, vp, vp, sz, ci, ci, ci, P, vp]),
             "sffft_to_bf16": (ci, [vp, vp, sz, vp]),
@@ -305,6 +306,37 @@ def conv_long(u, kf, plan: Plan, out=None, work=None):
     _check(fn(_ptr(u), _ptr(kf), _ptr(y), _ptr(work), wb, B, H, L, ctypes.byref(plan), _stream()),
            "sffft_conv_long")
     return y
+
+
+def spectrum_complex(k, L: int, plan: Plan, work=None):
+    """Kernel-order spectrum [H, 2L] of the complex filters k [H, L] (complex64, cuda) for a pair
+    plan (seqs = 2). conv(u, kf, plan) then computes the complex causal convolution of the
+    sequences whose real and imaginary planes are batch rows 2b' and 2b'+1 of u (see
+    complex_conv)."""
+    import torch
+
+    assert k.is_cuda and k.dtype == torch.complex64 and k.dim() == 2 and k.shape[1] == L
+    kr = k.real.contiguous()
+    ki = k.imag.contiguous()
+    H = k.shape[0]
+    kf = torch.empty((H, 2 * L), dtype=torch.complex64, device=k.device)
+    if work is None:
+        work = torch.empty_like(kf)
+    _check(lib().sffft_spectrum_complex(_ptr(kr), _ptr(ki), H, L, ctypes.byref(plan), _ptr(kf), _ptr(work),
+                                        _stream()), "sffft_spectrum_complex")
+    return kf
+
+
+def complex_conv(x, kf, plan: Plan):
+    """Complex causal convolution of x [Bc, H, L] complex64 (cuda) with the filters of
+    spectrum_complex(): the planes are interleaved as batch rows (2b', 2b'+1) = (Re, Im) of x[b'],
+    convolved with conv(), and reassembled."""
+    import torch
+
+    Bc, H, L = x.shape
+    u = torch.stack([x.real, x.imag], 1).reshape(2 * Bc, H, L).contiguous()
+    y = conv(u, kf, plan).reshape(Bc, 2, H, L)
+    return torch.complex(y[:, 0], y[:, 1])
 
 
 def spectrum_circular(k, plan: Plan, work=None):

@@ -339,9 +339,10 @@ __global__ void spectrum_stage_kernel(const float* __restrict__ k, float2* work,
 }
 
 // Gather into the fused kernel's order, folding in 1/sqrt(R_last) of the last
-// forward stage. src is p-order (natural == 0) or natural frequency order.
+// forward stage. src is p-order (natural == 0) or natural frequency order. With imag,
+// the gathered values are the spectrum of a filter's imaginary part: kf += i * value.
 __global__ void spectrum_permute_kernel(const float2* __restrict__ src, float2* __restrict__ kf, int H, int r0,
-                                        int r1, int r2, int mode, int natural, float scale) {
+                                        int r1, int r2, int mode, int natural, float scale, int imag = 0) {
   const int N = r0 * r1 * r2;
   const size_t gid = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (gid >= (size_t)H * N) return;
@@ -358,7 +359,12 @@ __global__ void spectrum_permute_kernel(const float2* __restrict__ src, float2* 
     s = natural ? k0 + r0 * k1 + r0 * r1 * k2 : k0 * (r1 * r2) + k1 * r2 + k2;
   }
   const float2 v = src[(size_t)h * N + s];
-  kf[gid] = make_float2(v.x * scale, v.y * scale);
+  if (imag) {
+    const float2 a = kf[gid];
+    kf[gid] = make_float2(a.x - v.y * scale, a.y + v.x * scale);
+  } else {
+    kf[gid] = make_float2(v.x * scale, v.y * scale);
+  }
 }
 
 __global__ void to_bf16_kernel(const float* __restrict__ x, uint16_t* __restrict__ y, size_t n) {
@@ -461,8 +467,9 @@ int long_plans_for(int L, const LongEntry** out, int cap) {
   return k;
 }
 
+// imag: k is the imaginary part of a complex filter; its spectrum is added times i to kf
 int spectrum_impl(const float* k, int H, int L, int klen, const sffft_plan* plan, void* kf, void* work,
-                  void* stream) {
+                  void* stream, int imag = 0) {
   if (!k || !kf || !work || H < 1 || kf == work) return SFFFT_EINVAL;
   const int rc = check_shape(L, plan);
   if (rc) return rc;
@@ -480,7 +487,7 @@ int spectrum_impl(const float* k, int H, int L, int klen, const sffft_plan* plan
   const size_t total = (size_t)H * N;
   hipLaunchKernelGGL(spectrum_permute_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s,
                      (const float2*)w, static_cast<float2*>(kf), H, plan->r0, plan->r1, plan->r2, plan->mode, 0,
-                     last_stage_scale(plan));
+                     last_stage_scale(plan), imag);
   return hip_status(hipGetLastError(), "spectrum permute launch");
 }
 }  // namespace
@@ -563,6 +570,14 @@ size_t sffft_spectrum_bytes(int H, int L) {
 
 int sffft_spectrum(const float* k, int H, int L, const sffft_plan* plan, void* kf, void* work, void* stream) {
   return spectrum_impl(k, H, L, L, plan, kf, work, stream);
+}
+
+int sffft_spectrum_complex(const float* kr, const float* ki, int H, int L, const sffft_plan* plan, void* kf,
+                           void* work, void* stream) {
+  // pairs of sequences per transform only: they carry the real and imaginary planes of u and y
+  if (!plan || plan->seqs != 2 || !ki || ki == kr) return SFFFT_EINVAL;
+  const int rc = spectrum_impl(kr, H, L, L, plan, kf, work, stream);
+  return rc ? rc : spectrum_impl(ki, H, L, L, plan, kf, work, stream, 1);
 }
 
 int sffft_spectrum_circular(const float* k, int H, int N, const sffft_plan* plan, void* kf, void* work,
