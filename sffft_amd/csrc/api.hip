@@ -50,23 +50,16 @@ size_t lds_bytes_rt(int r0, int r1, int r2, int mode, int channels, int waves) {
     return (size_t)(T1 * T1 * 64 + (r2 == r1 ? 0 : T2 * T2 * 64)) * 16 + (size_t)(r2 == r1 ? 1 : 2) * NR * 8;
   }
   if (mode == 1) {
-    // WavePlan::lds_bytes: DFT fragments and the twiddle tables (one when r0 == r1);
-    // then, in order of preference, row-load scratch and spectra; strided loads with
-    // spectra, the first fragment kind only and a one-round output scratch; or the
-    // row-load scratch alone (spectra read from global memory)
+    // WavePlan::lds_bytes: the twiddle tables (one when r0 == r1), the row-load scratch and,
+    // in order of preference, both DFT fragment kinds and the spectra; the first kind only
+    // and the spectra; or the first kind only (spectra read through L2)
     const int T0 = r0 / 16, T1 = r1 / 16, N = r0 * r1;
     const size_t frags = (size_t)(T0 * T0 * 128 + (r1 == r0 ? 0 : T1 * T1 * 128)) * 16;
     const size_t tw = (size_t)((r1 == r0 ? 1 : 2) * N / 2) * 16;
     const size_t scratch = (size_t)waves * 16 * (r1 + 4) * 4, spectra = (size_t)channels * N / 2 * 16;
-    const bool rows = frags + tw + spectra + scratch <= 163840 || frags + tw + spectra > 163840;
-    auto out_scratch = [&](int es) {
-      const int rr = 64 * (16 / es) / r1 < 16 ? 64 * (16 / es) / r1 : 16;
-      return (size_t)rr * (r1 + (es == 4 ? 4 : 8)) * es;
-    };
-    const size_t tab = rows ? frags + tw : frags / 2 + tw;
-    const size_t scr = rows ? scratch : (size_t)waves * std::max(out_scratch(4), out_scratch(2));
-    const bool in_lds = tab + spectra + scr <= 163840;
-    return tab + (in_lds ? spectra : 0) + scr;
+    const size_t tab = frags + tw + spectra + scratch <= 163840 ? frags + tw : frags / 2 + tw;
+    const bool in_lds = tab + spectra + scratch <= 163840;
+    return tab + (in_lds ? spectra : 0) + scratch;
   }
   const int S = r2 > 1 ? 3 : 2, N = r0 * r1 * r2, M = N / r0;
   const int PA = r1 + LDS_PAD, PB = r0 + LDS_PAD;

@@ -27,7 +27,7 @@
 // Read-only tables in LDS, filled once per workgroup:
 //   F0, F1 : DFT fragments of radix R0 and R1, both kinds ([cos | sin] and
 //            [-sin | cos]) in the order of the coefficient table (the first kind
-//            only in the strided layout, see WavePlan)
+//            only when both do not fit beside the spectra, see WavePlan)
 //   TW1    : sc0 * w^(m k0) in the lane order of the phase-1 result tiles
 //   TW2    : sc1 * sc0 * w^(k0 n1) in the lane order of the inverse result tiles
 // so no twiddle is evaluated in the loop and no per-stage scale is applied; the
@@ -61,26 +61,19 @@ struct WavePlan {
   static constexpr int TAB1_F4 = (F0_H8 + F1_H8) / 2 + TW_TABLES * TW_F4;
   // per-wavefront operand scratch of the row loads with fp32 I/O (bf16 needs less)
   static constexpr int SCRATCH_MAX = 16 * (M + 4) * 4;
-  // per-wavefront output scratch of one store round (1 KB of whole rows) for an I/O
-  // element of `es` bytes, at the pitch of the row scratch
-  static constexpr int out_rows(int es) { return 64 * (16 / es) / M < 16 ? 64 * (16 / es) / M : 16; }
-  static constexpr int out_scratch(int es) { return out_rows(es) * (M + (es == 4 ? 4 : 8)) * es; }
-  static constexpr int OUT_SCRATCH_MAX = out_scratch(4) > out_scratch(2) ? out_scratch(4) : out_scratch(2);
-  // Layout choice for a workgroup of nw wavefronts serving ch channels, in order of
-  // preference: row loads and spectra in LDS; strided loads, spectra in LDS, the
-  // first fragment kind only and an output scratch of one store round; row loads
-  // and spectra read from global memory.
-  static constexpr int tables_and_spectra_bytes(int ch) { return (TAB_F4 + ch * SP_F4) * 16; }
-  static constexpr bool row_loads(int ch, int nw) {
-    return tables_and_spectra_bytes(ch) + nw * SCRATCH_MAX <= 163840 || tables_and_spectra_bytes(ch) > 163840;
+  // Layout for a workgroup of nw wavefronts serving ch channels, in order of preference:
+  // both DFT fragment kinds and the spectra in LDS; the first kind only with the spectra
+  // in LDS; the first kind only with the spectra read through L2. Every layout reads the
+  // pairs as row chunks through the operand scratch.
+  static constexpr bool both_kinds(int ch, int nw) {
+    return (TAB_F4 + ch * SP_F4) * 16 + nw * SCRATCH_MAX <= 163840;
   }
-  static constexpr int tables_f4(int ch, int nw) { return row_loads(ch, nw) ? TAB_F4 : TAB1_F4; }
-  static constexpr int scratch_max(int ch, int nw) { return row_loads(ch, nw) ? SCRATCH_MAX : OUT_SCRATCH_MAX; }
+  static constexpr int tables_f4(int ch, int nw) { return both_kinds(ch, nw) ? TAB_F4 : TAB1_F4; }
   static constexpr bool spectra_in_lds(int ch, int nw) {
-    return (tables_f4(ch, nw) + ch * SP_F4) * 16 + nw * scratch_max(ch, nw) <= 163840;
+    return (tables_f4(ch, nw) + ch * SP_F4) * 16 + nw * SCRATCH_MAX <= 163840;
   }
   static constexpr int lds_bytes(int ch, int nw) {
-    return (tables_f4(ch, nw) + (spectra_in_lds(ch, nw) ? ch * SP_F4 : 0)) * 16 + nw * scratch_max(ch, nw);
+    return (tables_f4(ch, nw) + (spectra_in_lds(ch, nw) ? ch * SP_F4 : 0)) * 16 + nw * SCRATCH_MAX;
   }
   static_assert(R0 >= 16 && R0 <= 64 && R1 >= 16 && R1 <= 64, "radices are 16, 32 or 64");
 };
@@ -199,54 +192,22 @@ __device__ __forceinline__ void compute_dft(h8* dst, int tid) {
 // chunks, one KB per instruction, with the streaming (non-temporal) hint: chunk q of
 // the pair (rows a then b) goes to lane q % 64 of round q / 64.
 
-template <class P, class TIO, bool ROWS>
-struct PairLoads;
-
 template <class P, class TIO>
-struct PairLoads<P, TIO, true> {
+struct PairLoads {
   static constexpr int EPC = 16 / (int)sizeof(TIO);  // samples per chunk
   static constexpr int CPS = P::L / EPC;              // chunks per row
   static constexpr int ROUNDS = (2 * CPS + 63) / 64;  // load instructions per pair
-  static constexpr int ISSUES = ROUNDS;
   u32x4 c[ROUNDS];
 };
 
-// Strided loads (no LDS scratch): lane (r, g) loads its own operand elements,
-// n0 = 16ks + 4g + j, m = 16mt + r, one instruction per element (64-byte runs).
-template <class P, class TIO>
-struct PairLoads<P, TIO, false> {
-  static constexpr int ISSUES = P::MT * P::KS1 * 8;
-  TIO raw[P::MT][P::KS1][8];
-};
-
 // Vector-memory instructions issue_pair_loads emits.
-template <class P, class TIO, bool ROWS>
-__host__ __device__ constexpr int pair_load_issues() { return PairLoads<P, TIO, ROWS>::ISSUES; }
+template <class P, class TIO>
+__host__ __device__ constexpr int pair_load_issues() { return PairLoads<P, TIO>::ROUNDS; }
 
 template <class P, class TIO>
 __device__ __forceinline__ void issue_pair_loads(const TIO* __restrict__ xa, const TIO* __restrict__ xb,
-                                                 PairLoads<P, TIO, false>& d, int lane) {
-  constexpr int R0 = P::R0, M = P::M, MT = P::MT;
-  const int r = lane & 15, g = lane >> 4;
-  // lane bases at (n0 = 4g, m = r); every element is a constant offset from them
-  const TIO* pa = xa + (4 * g * M + r);
-  const TIO* pb = xb + (4 * g * M + r);
-  const bool live = R0 >= 32 || 4 * g < R0 / 2;  // R0 = 16: rows n0 >= 8 are the zero padding
-#pragma unroll
-  for (int mt = 0; mt < MT; mt++)
-#pragma unroll
-    for (int ks = 0; ks < P::KS1; ks++)
-#pragma unroll
-      for (int j = 0; j < 8; j++) {
-        const int off = (16 * ks + (j & 3)) * M + 16 * mt;
-        d.raw[mt][ks][j] = live ? (j < 4 ? pa[off] : pb[off]) : (TIO)0;
-      }
-}
-
-template <class P, class TIO>
-__device__ __forceinline__ void issue_pair_loads(const TIO* __restrict__ xa, const TIO* __restrict__ xb,
-                                                 PairLoads<P, TIO, true>& d, int lane) {
-  typedef PairLoads<P, TIO, true> D;
+                                                 PairLoads<P, TIO>& d, int lane) {
+  typedef PairLoads<P, TIO> D;
 #pragma unroll
   for (int i = 0; i < D::ROUNDS; i++) {
     const int q = i * 64 + lane;
@@ -271,34 +232,9 @@ __device__ __forceinline__ float io_to_f32_lds(const uint16_t* p) { return __uin
 
 // Phase-1 A operands a[mt][ks] (slots 0..3 row a, 4..7 row b; n0 = 16ks + 4g + j,
 // m = 16mt + r) from the pair's chunks, through the wave's scratch S.
-// 0 that the compiler cannot see through: added to the raw bits of the first pair's
-// strided operands, it keeps their conversion below the workgroup barrier (hoisted
-// above it, the conversion would make the wave wait for its loads there).
-__device__ __forceinline__ uint32_t opaque_zero() {
-  uint32_t v;
-  __asm__ volatile("v_mov_b32 %0, 0" : "=v"(v));
-  return v;
-}
-__device__ __forceinline__ float io_bits_to_f32(float x, uint32_t z) { return __uint_as_float(__float_as_uint(x) + z); }
-__device__ __forceinline__ float io_bits_to_f32(uint16_t x, uint32_t z) {
-  return __uint_as_float(((uint32_t)x + z) << 16);
-}
-
 template <class P, class TIO>
-__device__ __forceinline__ void pair_operands(const PairLoads<P, TIO, false>& d, TIO*, uint32_t z, h8 (*a)[P::KS1],
-                                              int) {
-#pragma unroll
-  for (int mt = 0; mt < P::MT; mt++)
-#pragma unroll
-    for (int ks = 0; ks < P::KS1; ks++)
-#pragma unroll
-      for (int j = 0; j < 8; j++) a[mt][ks][j] = (_Float16)io_bits_to_f32(d.raw[mt][ks][j], z);
-}
-
-template <class P, class TIO>
-__device__ __forceinline__ void pair_operands(const PairLoads<P, TIO, true>& d, TIO* S, uint32_t, h8 (*a)[P::KS1],
-                                              int lane) {
-  typedef PairLoads<P, TIO, true> D;
+__device__ __forceinline__ void pair_operands(const PairLoads<P, TIO>& d, TIO* S, h8 (*a)[P::KS1], int lane) {
+  typedef PairLoads<P, TIO> D;
   constexpr int R0 = P::R0, M = P::M, PITCH = scratch_pitch<P, TIO>();
   constexpr int ROWS = R0 / 2 < 16 ? R0 / 2 : 16;  // non-zero rows per K step
   const int r = lane & 15, g = lane >> 4;
@@ -366,40 +302,13 @@ __device__ __forceinline__ void store_rows(TIO* S, const f4 (&z)[P::MT], TIO* __
   __asm__ volatile("" ::: "memory");
 }
 
-// The same through a scratch of one store round only (the strided layout): the
-// 16-row block goes out in rounds of P::out_rows rows (1 KB, whole rows), each staged
-// by the 16 lanes that hold those rows.
-template <class P, class TIO>
-__device__ __forceinline__ void store_rounds(TIO* S, const f4 (&z)[P::MT], TIO* __restrict__ y, int lane) {
-  constexpr int M = P::M, PITCH = scratch_pitch<P, TIO>(), EPC = 16 / (int)sizeof(TIO), CPR = M / EPC;
-  constexpr int RPR = P::out_rows((int)sizeof(TIO));
-  static_assert(P::R0 >= 32 && 16 % RPR == 0 && RPR * CPR <= 64, "16 stored rows in whole rounds");
-  const int c = lane & 15, g = lane >> 4;
-#pragma unroll
-  for (int q = 0; q < 16 / RPR; q++) {
-    if (c / RPR == q) {
-#pragma unroll
-      for (int t = 0; t < P::MT; t++) put4(S + (c % RPR) * PITCH + 16 * t + 4 * g, z[t]);
-    }
-    // other lanes' writes are read below, and the next round's writes follow these
-    // reads (see pair_operands)
-    __asm__ volatile("" ::: "memory");
-    const int row = lane / CPR, col = (lane % CPR) * EPC;
-    if (RPR * CPR == 64 || row < RPR)
-      __builtin_nontemporal_store(*reinterpret_cast<const u32x4*>(S + row * PITCH + col),
-                                  reinterpret_cast<u32x4*>(y + (q * RPR + row) * M + col));
-    __asm__ volatile("" ::: "memory");
-  }
-}
-
 // Every stage of one pair, from its loaded operands to the stored outputs; SP is the
 // channel's spectrum in LDS.
-template <class P, class TIO, bool ACC16, bool HOLD_F1, bool ROWS>
-__device__ __forceinline__ void process_pair(const PairLoads<P, TIO, ROWS>& d, TIO* S, uint32_t z, const float4* SP,
+template <class P, class TIO, bool ACC16, bool HOLD_F1, bool K1>
+__device__ __forceinline__ void process_pair(const PairLoads<P, TIO>& d, TIO* S, const float4* SP,
                                              TIO* __restrict__ ya, TIO* __restrict__ yb, const h8* F0,
                                              const h8* F1, const float4* TW1, const float4* TW2, int lane) {
   constexpr int R0 = P::R0, M = P::M, MT = P::MT, ST = P::ST, KS1 = P::KS1, NT3 = P::NT3;
-  constexpr bool K1 = !ROWS;  // the strided layout keeps the first fragment kind only
   // With 16 tiles per transform (64x64) the pair alone fills 64 VGPRs; compiler-only
   // barriers at the top of each tile step keep the next step's table and spectrum
   // loads from being hoisted over the current one, which would not fit beside it.
@@ -410,7 +319,7 @@ __device__ __forceinline__ void process_pair(const PairLoads<P, TIO, ROWS>& d, T
 
   // ---- phase 1: DFT over n0 (first R0/2 rows only), twiddle, -> B2[m tile][k0 strip]
   h8 a[MT][KS1];
-  pair_operands<P, TIO>(d, S, z, a, lane);
+  pair_operands<P, TIO>(d, S, a, lane);
   h8 b2[MT][ST];
 #pragma unroll
   for (int nt = 0; nt < ST; nt++) {
@@ -487,44 +396,25 @@ __device__ __forceinline__ void process_pair(const PairLoads<P, TIO, ROWS>& d, T
 #pragma unroll
   for (int nu = 0; nu < NT3; nu++) {
     step_fence();
-    if constexpr (ROWS) {
-      h8 f0[ST], f1[ST];
+    h8 f0[ST], f1[ST];
+#pragma unroll
+    for (int s = 0; s < ST; s++) {
+      f0[s] = dft_frag<R0, K1>(F0, nu, s, 0, lane);
+      f1[s] = dft_frag<R0, K1>(F0, nu, s, 1, lane);
+    }
+    f4 za[MT] = {}, zb[MT] = {};
+#pragma unroll
+    for (int t = 0; t < MT; t++) {
 #pragma unroll
       for (int s = 0; s < ST; s++) {
-        f0[s] = dft_frag<R0, K1>(F0, nu, s, 0, lane);
-        f1[s] = dft_frag<R0, K1>(F0, nu, s, 1, lane);
+        za[t] = mfma(b2[t][s], f0[s], za[t]);
+        zb[t] = mfma(b2[t][s], f1[s], zb[t]);
       }
-      f4 za[MT] = {}, zb[MT] = {};
-#pragma unroll
-      for (int t = 0; t < MT; t++) {
-#pragma unroll
-        for (int s = 0; s < ST; s++) {
-          za[t] = mfma(b2[t][s], f0[s], za[t]);
-          zb[t] = mfma(b2[t][s], f1[s], zb[t]);
-        }
-        za[t] = acc_round<ACC16>(za[t]);
-        zb[t] = -acc_round<ACC16>(zb[t]);  // row b is minus the imaginary part
-      }
-      store_rows<P, TIO>(S, za, ya + 16 * nu * M, lane);
-      store_rows<P, TIO>(S, zb, yb + 16 * nu * M, lane);
-    } else {
-      // one row at a time: its 16-row block stays live through the store rounds, so
-      // the other row's fragments and results are not made before it is stored
-#pragma unroll
-      for (int kind = 0; kind < 2; kind++) {
-        h8 f[ST];
-#pragma unroll
-        for (int s = 0; s < ST; s++) f[s] = dft_frag<R0, K1>(F0, nu, s, kind, lane);
-        f4 z[MT] = {};
-#pragma unroll
-        for (int t = 0; t < MT; t++) {
-#pragma unroll
-          for (int s = 0; s < ST; s++) z[t] = mfma(b2[t][s], f[s], z[t]);
-          z[t] = kind == 0 ? acc_round<ACC16>(z[t]) : -acc_round<ACC16>(z[t]);
-        }
-        store_rounds<P, TIO>(S, z, (kind == 0 ? ya : yb) + 16 * nu * M, lane);
-      }
+      za[t] = acc_round<ACC16>(za[t]);
+      zb[t] = -acc_round<ACC16>(zb[t]);  // row b is minus the imaginary part
     }
+    store_rows<P, TIO>(S, za, ya + 16 * nu * M, lane);
+    store_rows<P, TIO>(S, zb, yb + 16 * nu * M, lane);
   }
 }
 
@@ -538,8 +428,8 @@ __global__ void __launch_bounds__(64 * NW)
     fftconv_wave_kernel(const TIO* __restrict__ u, const float4* __restrict__ kf, TIO* __restrict__ y, int B,
                         int H, const h8* __restrict__ ftab, const float4* __restrict__ twtab) {
   constexpr int R0 = P::R0;
-  constexpr bool ROWS = P::row_loads(CH, NW), K1 = !ROWS;
-  constexpr int SCR_F4 = (ROWS ? scratch_bytes<P, TIO>() : P::out_scratch((int)sizeof(TIO))) / 16;
+  constexpr bool K1 = !P::both_kinds(CH, NW);  // first DFT fragment kind only
+  constexpr int SCR_F4 = scratch_bytes<P, TIO>() / 16;
   constexpr bool SP_LDS = P::spectra_in_lds(CH, NW);
   constexpr int SPL_F4 = SP_LDS ? CH * P::SP_F4 : 0, TAB_F4 = P::tables_f4(CH, NW);
   constexpr int F0_H8 = K1 ? P::F0_H8 / 2 : P::F0_H8, F1_H8 = K1 ? P::F1_H8 / 2 : P::F1_H8;
@@ -594,7 +484,7 @@ __global__ void __launch_bounds__(64 * NW)
   // after the barrier, so the first channel's data lands (and is computed and
   // stored) while the rest is still in flight.
   const int npairs = nch * BP;
-  PairLoads<P, TIO, ROWS> cur;
+  PairLoads<P, TIO> cur;
   auto issue_first = [&]() {
     const int c = wave / BP, bp = wave - c * BP;
     const size_t ra = ((size_t)(2 * bp) * H + h0 + c) * P::L;
@@ -604,7 +494,7 @@ __global__ void __launch_bounds__(64 * NW)
   __asm__ volatile("" ::: "memory");
   if (early) {
     issue_first();
-    wait_vmcnt<pair_load_issues<P, TIO, ROWS>()>();
+    wait_vmcnt<pair_load_issues<P, TIO>()>();
   } else {
     wait_vmcnt<0>();
   }
@@ -620,8 +510,7 @@ __global__ void __launch_bounds__(64 * NW)
   if (wave < npairs) {
     const int c = wave / BP, bp = wave - c * BP;
     const size_t ra = ((size_t)(2 * bp) * H + h0 + c) * P::L, rb = ra + (size_t)H * P::L;
-    process_pair<P, TIO, ACC16, HOLD>(cur, S, ROWS ? 0u : opaque_zero(), spec(c), y + ra, y + rb, F0, F1, TW1, TW2,
-                                      lane);
+    process_pair<P, TIO, ACC16, HOLD, K1>(cur, S, spec(c), y + ra, y + rb, F0, F1, TW1, TW2, lane);
   }
   for (int p = wave + NW; p < npairs; p += NW) {
     // compiler-only barrier: keeps the table reads inside the loop (hoisting them
@@ -635,7 +524,7 @@ __global__ void __launch_bounds__(64 * NW)
     const int c = p / BP, bp = p - c * BP;
     const size_t ra = ((size_t)(2 * bp) * H + h0 + c) * P::L, rb = ra + (size_t)H * P::L;
     issue_pair_loads<P, TIO>(u + ra, u + rb, cur, ln);
-    process_pair<P, TIO, ACC16, HOLD>(cur, S, 0u, spec(c), y + ra, y + rb, F0, F1, TW1, TW2, ln);
+    process_pair<P, TIO, ACC16, HOLD, K1>(cur, S, spec(c), y + ra, y + rb, F0, F1, TW1, TW2, ln);
   }
 }
 
