@@ -148,6 +148,37 @@ int sffft_circconv_long_f32(const float* u, const void* kf, float* y, void* work
 int sffft_circconv_long_bf16(const uint16_t* u, const void* kf, uint16_t* y, void* work, size_t work_bytes, int B,
                              int H, int N, const sffft_plan* plan, void* stream);
 
+/* Standalone complex transforms. The reference lists standalone forward/inverse FFTs and
+ * 2-D convolution as not exposed (README.md:174); no counterpart. Complex64 in and out,
+ * unnormalised:
+ *   X[b,k] = scale * sum_{n<N} x[b,n] * exp(-/+ 2 pi i n k / N)
+ * with the minus sign for inverse = 0 and the plus sign for inverse = 1. N is a power of two
+ * in [2, 2^24] and batch * N <= 2^31. Element n of sequence b sits at x[b * dist + n * stride]
+ * (complex elements, stride >= 1, dist >= 1 when batch > 1); X has the same layout and may
+ * equal x. `work` holds sffft_fft_work_bytes(batch, N) bytes (NULL allowed when that is 0) and
+ * must not overlap x or X. Each stage is a radix-<=64 DFT evaluated in fp64 and stored as
+ * complex64 (relative error ~1e-7); pointers 8-byte aligned. sffft_fft_work_bytes returns 0
+ * for sizes the call rejects. */
+size_t sffft_fft_work_bytes(int batch, int N);
+int sffft_fft_c2c(const void* x, void* X, void* work, size_t work_bytes, int batch, int N, long long stride,
+                  long long dist, int inverse, float scale, void* stream);
+
+/* 2-D transform of `batch` contiguous [N0][N1] complex64 arrays (every row, then every
+ * column), same sign, scale, size and aliasing rules as sffft_fft_c2c per axis, and
+ * batch * N0 * N1 <= 2^31. `work`: sffft_fft2_work_bytes(batch, N0, N1) bytes. */
+size_t sffft_fft2_work_bytes(int batch, int N0, int N1);
+int sffft_fft2_c2c(const void* x, void* X, void* work, size_t work_bytes, int batch, int N0, int N1, int inverse,
+                   float scale, void* stream);
+
+/* 2-D circular convolution of period (N0, N1), fp32 in and out:
+ *   y[b,h,i,j] = sum_{a<N0, c<N1} u[b,h,a,c] * k[h,(i-a) mod N0,(j-c) mod N1]
+ * u, y [B][H][N0][N1], k [H][N0][N1], through 2-D transforms as sffft_fft2_c2c (complex
+ * spectrum product, inverse, real part). `work` holds sffft_circconv2d_work_bytes(B, H, N0,
+ * N1) bytes and must not overlap u, k or y; y may not overlap u or k. */
+size_t sffft_circconv2d_work_bytes(int B, int H, int N0, int N1);
+int sffft_circconv2d_f32(const float* u, const float* k, float* y, void* work, size_t work_bytes, int B, int H,
+                         int N0, int N1, void* stream);
+
 /* fp32 -> bf16 (round to nearest even) on the device. Replaces tobf16 (src/sffft.cu:306). */
 int sffft_to_bf16(const float* x, uint16_t* y, size_t n, void* stream);
 

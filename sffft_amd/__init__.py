@@ -111,6 +111,13 @@ def lib() -> ctypes.CDLL:
             "sffft_spectrum_complex": (ci, [vp, vp, ci, ci, P, vp, vp, vp]),
             "sffft_circconv_long_f32": (ci, [vp, vp, vp, vp, sz, ci, ci, ci, P, vp]),
             "sffft_circconv_long_bf16": (ci, [vp, vp, vp, vp, sz, ci, ci, ci, P, vp]),
+            "sffft_fft_work_bytes": (sz, [ci, ci]),
+            "sffft_fft_c2c": (ci, [vp, vp, vp, sz, ci, ci, ctypes.c_longlong, ctypes.c_longlong, ci,
+                                   ctypes.c_float, vp]),
+            "sffft_fft2_work_bytes": (sz, [ci, ci, ci]),
+            "sffft_fft2_c2c": (ci, [vp, vp, vp, sz, ci, ci, ci, ci, ctypes.c_float, vp]),
+            "sffft_circconv2d_work_bytes": (sz, [ci, ci, ci, ci]),
+            "sffft_circconv2d_f32": (ci, [vp, vp, vp, vp, sz, ci, ci, ci, ci, vp]),
             "sffft_to_bf16": (ci, [vp, vp, sz, vp]),
             "sffft_dispatch_floor": (ci, [ci, ci, ci, P, vp]),
             "sffft_dft_table": (ci, [vp, sz]),
@@ -375,6 +382,69 @@ def circconv(u, kf, plan: Plan, out=None, work=None):
     wb = work.numel() * work.element_size()
     _check(fn(_ptr(u), _ptr(kf), _ptr(y), _ptr(work), wb, B, H, N, ctypes.byref(plan), _stream()),
            "sffft_circconv_long")
+    return y
+
+
+def _work(nbytes: int, device):
+    import torch
+
+    return torch.empty(max(nbytes, 16), dtype=torch.uint8, device=device)
+
+
+def fft(x, inverse: bool = False, scale: float = 1.0, dim: int = -1, out=None):
+    """Unnormalised complex transform of x (complex64, cuda) along `dim`:
+    X[k] = scale * sum_n x[n] exp(-/+ 2 pi i n k / N), minus sign forward, plus inverse.
+    dim -1 on any shape, or dim 0 of a 2-D tensor (its columns, read in place with
+    stride = columns). N a power of two in [2, 2^24]. `out` may be x."""
+    import torch
+
+    assert x.is_cuda and x.dtype == torch.complex64
+    x = x.contiguous()
+    if dim in (-1, x.dim() - 1):
+        N = x.shape[-1]
+        batch, stride, dist = x.numel() // N, 1, N
+    elif dim == 0 and x.dim() == 2:
+        N, batch = x.shape
+        stride, dist = batch, 1
+    else:
+        raise ValueError("fft: dim must be the last dimension, or 0 of a 2-D tensor")
+    X = torch.empty_like(x) if out is None else out
+    assert X.shape == x.shape and X.dtype == x.dtype and X.is_contiguous()
+    work = _work(lib().sffft_fft_work_bytes(batch, N), x.device)
+    _check(lib().sffft_fft_c2c(_ptr(x), _ptr(X), _ptr(work), work.numel(), batch, N, stride, dist, int(inverse),
+                               scale, _stream()), "sffft_fft_c2c")
+    return X
+
+
+def fft2(x, inverse: bool = False, scale: float = 1.0, out=None):
+    """Unnormalised 2-D transform over the last two dimensions of x [..., N0, N1]
+    (complex64, cuda), signs as fft(). `out` may be x."""
+    import torch
+
+    assert x.is_cuda and x.dtype == torch.complex64 and x.dim() >= 2
+    x = x.contiguous()
+    N0, N1 = x.shape[-2:]
+    batch = x.numel() // (N0 * N1)
+    X = torch.empty_like(x) if out is None else out
+    assert X.shape == x.shape and X.dtype == x.dtype and X.is_contiguous()
+    work = _work(lib().sffft_fft2_work_bytes(batch, N0, N1), x.device)
+    _check(lib().sffft_fft2_c2c(_ptr(x), _ptr(X), _ptr(work), work.numel(), batch, N0, N1, int(inverse), scale,
+                                _stream()), "sffft_fft2_c2c")
+    return X
+
+
+def circconv2d(u, k):
+    """2-D circular convolution of period (N0, N1): u [B, H, N0, N1], k [H, N0, N1], fp32 cuda."""
+    import torch
+
+    assert u.is_cuda and u.dtype == torch.float32 and k.dtype == torch.float32 and u.dim() == 4
+    u, k = u.contiguous(), k.contiguous()
+    B, H, N0, N1 = u.shape
+    assert tuple(k.shape) == (H, N0, N1)
+    y = torch.empty_like(u)
+    work = _work(lib().sffft_circconv2d_work_bytes(B, H, N0, N1), u.device)
+    _check(lib().sffft_circconv2d_f32(_ptr(u), _ptr(k), _ptr(y), _ptr(work), work.numel(), B, H, N0, N1, _stream()),
+           "sffft_circconv2d_f32")
     return y
 
 

@@ -15,6 +15,7 @@
 #include "fftconv_wave.hpp"
 #include "longconv.hpp"
 #include "registry.hpp"
+#include "transforms.hpp"
 
 namespace sffft {
 namespace {
@@ -647,6 +648,107 @@ int sffft_dispatch_floor(int B, int H, int L, const sffft_plan* plan, void* stre
   hipLaunchKernelGGL(empty_dispatch_kernel, dim3(grid), dim3(64 * plan->waves), (unsigned)e->lds_bytes,
                      (hipStream_t)stream);
   return hip_status(hipGetLastError(), "dispatch floor launch");
+}
+
+namespace {
+bool span_overlap(const void* a, size_t na, const void* b, size_t nb) {
+  const uintptr_t x = (uintptr_t)a, z = (uintptr_t)b;
+  return na && nb && x < z + nb && z < x + na;
+}
+bool aligned8(const void* p) { return ((uintptr_t)p & 7u) == 0; }
+
+// Validated 1-D transform layout; *elems: extent of x / X in complex elements.
+int fft_layout(int batch, int N, long long stride, long long dist, xf::Seqs* q, long long* extent) {
+  xf::Radices d;
+  if (batch < 1 || !xf::split(N, &d) || (long long)batch * N > xf::MAX_ELEMS) return SFFFT_EINVAL;
+  if (stride < 1 || dist < 0 || (batch > 1 && dist < 1)) return SFFFT_EINVAL;
+  *q = xf::Seqs{batch, batch, dist, 0, stride, dist < stride ? 1 : 0};
+  *extent = (long long)(batch - 1) * dist + (long long)(N - 1) * stride + 1;
+  return SFFFT_OK;
+}
+
+int fft2_layout(int batch, int N0, int N1, long long* elems, long long* work) {
+  xf::Radices d;
+  if (batch < 1 || !xf::split(N0, &d) || !xf::split(N1, &d)) return SFFFT_EINVAL;
+  const long long n = (long long)batch * N0 * N1;
+  if (n > xf::MAX_ELEMS) return SFFFT_EINVAL;
+  *elems = n;
+  *work = xf::work2_elems(batch, N0, N1);
+  return SFFFT_OK;
+}
+
+int circconv2d_layout(int B, int H, int N0, int N1, long long* elems, long long* work) {
+  xf::Radices d;
+  if (B < 1 || H < 1 || !xf::split(N0, &d) || !xf::split(N1, &d)) return SFFFT_EINVAL;
+  const long long n = (long long)B * H * N0 * N1;
+  if (n > xf::MAX_ELEMS) return SFFFT_EINVAL;
+  *elems = n;
+  *work = xf::circconv2d_elems(B, H, N0, N1);
+  return SFFFT_OK;
+}
+}  // namespace
+
+size_t sffft_fft_work_bytes(int batch, int N) {
+  xf::Seqs q;
+  long long ext;
+  if (fft_layout(batch, N, 1, N, &q, &ext)) return 0;
+  return (size_t)xf::work_elems(q, N) * 8;
+}
+
+int sffft_fft_c2c(const void* x, void* X, void* work, size_t work_bytes, int batch, int N, long long stride,
+                  long long dist, int inverse, float scale, void* stream) {
+  xf::Seqs q;
+  long long ext;
+  if (!x || !X || !aligned8(x) || !aligned8(X) || (inverse != 0 && inverse != 1)) return SFFFT_EINVAL;
+  if (fft_layout(batch, N, stride, dist, &q, &ext)) return SFFFT_EINVAL;
+  const size_t need = (size_t)xf::work_elems(q, N) * 8;
+  if (need && (!work || !aligned8(work) || work_bytes < need || span_overlap(work, need, x, ext * 8) ||
+               span_overlap(work, need, X, ext * 8)))
+    return SFFFT_EINVAL;
+  return hip_status(xf::run(static_cast<const float2*>(x), static_cast<float2*>(X), static_cast<float2*>(work), q, N,
+                            inverse, scale, (hipStream_t)stream),
+                    "fft launch");
+}
+
+size_t sffft_fft2_work_bytes(int batch, int N0, int N1) {
+  long long n, w;
+  if (fft2_layout(batch, N0, N1, &n, &w)) return 0;
+  return (size_t)w * 8;
+}
+
+int sffft_fft2_c2c(const void* x, void* X, void* work, size_t work_bytes, int batch, int N0, int N1, int inverse,
+                   float scale, void* stream) {
+  long long n, w;
+  if (!x || !X || !aligned8(x) || !aligned8(X) || (inverse != 0 && inverse != 1)) return SFFFT_EINVAL;
+  if (fft2_layout(batch, N0, N1, &n, &w)) return SFFFT_EINVAL;
+  const size_t need = (size_t)w * 8, bytes = (size_t)n * 8;
+  if (x != X && span_overlap(x, bytes, X, bytes)) return SFFFT_EINVAL;  // partial overlap
+  if (need && (!work || !aligned8(work) || work_bytes < need || span_overlap(work, need, x, bytes) ||
+               span_overlap(work, need, X, bytes)))
+    return SFFFT_EINVAL;
+  return hip_status(xf::run2(static_cast<const float2*>(x), static_cast<float2*>(X), static_cast<float2*>(work), batch,
+                             N0, N1, inverse, scale, (hipStream_t)stream),
+                    "fft2 launch");
+}
+
+size_t sffft_circconv2d_work_bytes(int B, int H, int N0, int N1) {
+  long long n, w;
+  if (circconv2d_layout(B, H, N0, N1, &n, &w)) return 0;
+  return (size_t)w * 8;
+}
+
+int sffft_circconv2d_f32(const float* u, const float* k, float* y, void* work, size_t work_bytes, int B, int H,
+                         int N0, int N1, void* stream) {
+  long long n, w;
+  if (!u || !k || !y || !work || !aligned16(u) || !aligned16(k) || !aligned16(y) || !aligned16(work))
+    return SFFFT_EINVAL;
+  if (circconv2d_layout(B, H, N0, N1, &n, &w)) return SFFFT_EINVAL;
+  const size_t need = (size_t)w * 8, io = (size_t)n * 4, kb = (size_t)H * N0 * N1 * 4;
+  if (work_bytes < need || span_overlap(work, need, u, io) || span_overlap(work, need, y, io) ||
+      span_overlap(work, need, k, kb) || span_overlap(y, io, u, io) || span_overlap(y, io, k, kb))
+    return SFFFT_EINVAL;
+  return hip_status(xf::circconv2d(u, k, y, static_cast<float2*>(work), B, H, N0, N1, (hipStream_t)stream),
+                    "circconv2d launch");
 }
 
 int sffft_to_bf16(const float* x, uint16_t* y, size_t n, void* stream) {
