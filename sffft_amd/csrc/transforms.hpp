@@ -6,7 +6,7 @@
 // in fp64 with exact fp64 twiddles and stored as complex64 between stages (relative
 // error ~1e-7). The fused convolution kernels, with fp16 MFMA operands, are separate.
 //
-// Algorithm: N = r[0] * r[1] * ... * r[S-1] (powers of two, 64s first). Decimation in
+// Algorithm: N = r[0] * r[1] * ... * r[S-1] (powers of two, 16s first). Decimation in
 // frequency: stage J transforms digit J (stride s_J = r[J+1] * ... * r[S-1]) and, before
 // the next stage, multiplies by w_{r[J] s_J}^(k_J * (p mod s_J)). After the last stage
 // position p = sum_J k_J s_J holds frequency k = k_0 + r[0] (k_1 + r[1] (k_2 + ...)), so
@@ -20,23 +20,35 @@
 namespace sffft {
 namespace xf {
 
-constexpr int MAX_STAGES = 4;              // N <= 64^4
+#ifndef SFFFT_XF_MAX_RADIX
+#define SFFFT_XF_MAX_RADIX 16
+#endif
+constexpr int MAX_RADIX = SFFFT_XF_MAX_RADIX;
+constexpr int MAX_STAGES = 6;
 constexpr long long MAX_N = 1LL << 24;
 constexpr long long MAX_ELEMS = 1LL << 31;  // sequences * N per call
+
+constexpr bool stages_cover_max_n() {
+  long long n = 1;
+  for (int i = 0; i < MAX_STAGES; i++) n *= MAX_RADIX;
+  return n >= MAX_N;
+}
+static_assert(stages_cover_max_n(), "MAX_STAGES stages of MAX_RADIX must reach MAX_N");
 
 struct Radices {
   int S;
   int r[MAX_STAGES];
 };
 
-// N a power of two in [2, 2^24]: radix-64 stages, then the remainder.
+// N a power of two in [2, 2^24]: radix-MAX_RADIX stages, then the remainder.
 inline bool split(long long N, Radices* out) {
   if (N < 2 || N > MAX_N || (N & (N - 1))) return false;
-  Radices d{0, {1, 1, 1, 1}};
+  Radices d{0, {1, 1, 1, 1, 1, 1}};
   long long rest = N;
-  while (rest > 64) {
-    d.r[d.S++] = 64;
-    rest /= 64;
+  while (rest > MAX_RADIX) {
+    if (d.S == MAX_STAGES - 1) return false;  // never write past r[MAX_STAGES - 1]
+    d.r[d.S++] = MAX_RADIX;
+    rest /= MAX_RADIX;
   }
   d.r[d.S++] = (int)rest;
   *out = d;

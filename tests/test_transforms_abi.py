@@ -7,12 +7,12 @@ import sffft_amd as sf
 
 def test_work_bytes():
     lib = sf.lib()
-    assert lib.sffft_fft_work_bytes(4, 64) == 0  # one stage: no workspace
+    assert lib.sffft_fft_work_bytes(4, 16) == 0  # one stage: no workspace
     assert lib.sffft_fft_work_bytes(4, 128) == 4 * 128 * 8
     assert lib.sffft_fft_work_bytes(4, 96) == 0  # not a power of two: rejected
     assert lib.sffft_fft_work_bytes(1, 1 << 25) == 0
     assert lib.sffft_fft_work_bytes(0, 64) == 0
-    assert lib.sffft_fft2_work_bytes(2, 64, 64) == 0
+    assert lib.sffft_fft2_work_bytes(2, 16, 8) == 0
     assert lib.sffft_fft2_work_bytes(2, 64, 128) == 2 * 64 * 128 * 8
     assert lib.sffft_circconv2d_work_bytes(2, 3, 64, 128) == (2 * 3 + 3 + 2 * 3) * 64 * 128 * 8
     assert lib.sffft_circconv2d_work_bytes(2, 3, 64, 100) == 0
