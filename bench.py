@@ -1,17 +1,25 @@
 #!/usr/bin/env python3
 """Benchmark of the fused causal long convolution on one MI355X.
 
-Metric: ms per B=8 x H=768 batch (one fused launch = one step) at the workload
-L=1024, fp32 I/O: u ~ N(0,1) [8,768,1024], k ~ N(0,1) exp(-n/256)/sqrt(L) [768,1024],
-N=2048 two-stage 64x32 plan. Inputs are synthetic and resident in HBM before the
-timed region. By default every step uses another of several disjoint (u, y, spectrum)
-buffer sets totalling more than 512 MB, so the 256 MB Infinity Cache cannot hold
-the working set across steps (the warm, single-buffer time is reported beside it).
+Metric: ms per B=8 x H=768 batch vs L (fp32/bf16 I/O), % of the HBM roofline, rel-L2
+error. One step = one fused launch over one batch. The headline (`value`) is the
+workload L=1024, fp32 I/O: u ~ N(0,1) [8,768,1024], k ~ N(0,1) exp(-n/256)/sqrt(L)
+[768,1024], N=2048 two-stage 64x32 plan. The `sweep` key carries every L from 128 to
+8192 in fp32 and bf16 I/O (the reference's README table, src/sffft.cu:506-513), each
+beside the rocFFT pad/R2C/multiply/C2R/slice pipeline timed the same way.
+
+Inputs are synthetic and resident in HBM before the timed region. Every step uses
+another of several disjoint (u, y, spectrum) buffer sets totalling more than 512 MB, so
+the 256 MB Infinity Cache cannot hold the working set across steps (the warm,
+single-buffer time is reported beside it). The K steps are captured once as a HIP graph;
+before the start event the stream runs a spin kernel long enough for the host to enqueue
+the whole replay, so the events bracket back-to-back dispatches only, not the host's
+launch latency.
 
 Prints ONE JSON line (rank 0). Roofline: algorithmic bytes per launch =
-B*H*L*(in+out bytes) + H*2L*8 (u read once, y written once, complex64 spectrum
-read once) divided by the average launch duration measured with HIP events on the
-launch stream, against 8 TB/s.
+B*H*L*(in+out bytes) + H*2L*8 (u read once, y written once, complex64 spectrum read
+once) divided by the average launch duration measured with HIP events on the launch
+stream, against 8 TB/s.
 """
 from __future__ import annotations
 
@@ -25,6 +33,7 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
+SWEEP_LENGTHS = (128, 256, 512, 1024, 2048, 4096, 8192)
 
 
 def parse():
@@ -44,9 +53,12 @@ def parse():
     ap.add_argument("--acc", type=int, default=0)
     ap.add_argument("--rotate-mb", type=float, default=600.0,
                     help="minimum total size of the rotated buffer sets (0 = one warm set)")
+    ap.add_argument("--sweep", type=int, default=1,
+                    help="also time every L of the reference table (128..8192) in fp32 and bf16 I/O "
+                         "with the rocFFT pipeline beside each (the `sweep` key)")
     ap.add_argument("--cpu-baseline", type=int, default=1, help="time the fp64 CPU baseline (rank 0, N=1)")
-    ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU sample budget (seconds)")
-    ap.add_argument("--check", type=int, default=1, help="verify the output against the fp64 oracle")
+    ap.add_argument("--cpu-seconds", type=float, default=8.0, help="CPU sample budget per leg (seconds)")
+    ap.add_argument("--check", type=int, default=1, help="verify every output against the fp64 oracle")
     ap.add_argument("--work-mb", type=float, default=0.0,
                     help="multi-pass plans: workspace size in MB (0: the library's default chunking)")
     ap.add_argument("--copy-mb", type=float, default=0.0,
@@ -55,11 +67,12 @@ def parse():
     return ap.parse_args()
 
 
-def profiled_traffic(workload: str, plan) -> "int | None":
+def profiled_traffic(workload: str, plan, stamp: str) -> "int | None":
     """HBM bytes per launch measured by rocprofv3 PMC runs (FETCH_SIZE, WRITE_SIZE,
     calibrated on a plain copy) for this workload and plan, from the committed
-    summaries under profiles/ (their `workload:`, `plan:` and
-    `traffic_bytes_per_launch:` lines); None when no summary covers them."""
+    summaries under profiles/ (their `workload:`, `plan:`, `kernel_sources_sha:` and
+    `traffic_bytes_per_launch:` lines). Only a summary measured on a build of the same
+    kernel sources counts; None otherwise."""
     import glob
     import re
 
@@ -67,11 +80,75 @@ def profiled_traffic(workload: str, plan) -> "int | None":
                  f"channels={plan.channels}")
     for path in sorted(glob.glob(os.path.join(ROOT, "profiles", "*.md"))):
         text = open(path).read()
-        if f"workload: {workload}\n" in text and want_plan + "\n" in text:
+        if (f"workload: {workload}\n" in text and want_plan + "\n" in text
+                and f"kernel_sources_sha: {stamp}\n" in text):
             m = re.search(r"^traffic_bytes_per_launch: (\d+)$", text, re.M)
             if m:
                 return int(m.group(1))
     return None
+
+
+class Cover:
+    """A spin kernel (torch.cuda._sleep) queued ahead of a timed region keeps the GPU busy
+    while the host enqueues the region's launches, so the start event is followed by
+    back-to-back dispatches and the host's launch latency stays outside the events."""
+
+    def __init__(self):
+        import torch
+
+        self.torch = torch
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda._sleep(1 << 16)  # first launch loads the kernel
+        e0.record()
+        torch.cuda._sleep(1 << 22)
+        e1.record()
+        torch.cuda.synchronize()
+        self.cycles_per_ms = (1 << 22) / max(e0.elapsed_time(e1), 1e-3)
+
+    def __call__(self, ms: float) -> None:
+        self.torch.cuda._sleep(int(self.cycles_per_ms * ms))
+
+
+def events_ms(cover, fn, reps, host_ms):
+    """Average ms per rep of fn() between two events on the current stream, with the
+    spin kernel covering the host's enqueue time (host_ms, measured beforehand)."""
+    import torch
+
+    torch.cuda.synchronize()
+    cover(max(0.3, 3.0 * host_ms + 0.1))
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    fn()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / reps
+
+
+def host_time_ms(fn):
+    import torch
+
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    fn()
+    t1 = time.perf_counter()
+    torch.cuda.synchronize()
+    return (t1 - t0) * 1e3
+
+
+def reference_protocol_ms(cover, fn, L):
+    """src/sffft.cu:321-327: 3 warm-ups, synchronise, an event pair around
+    clamp(20000/L, 10, 200) back-to-back launches on one buffer set. The launches are
+    eager, as in the reference; the spin kernel covers their host enqueue time so the
+    events see the GPU's back-to-back dispatches (the reference enqueues from C++, whose
+    launch rate keeps ahead of the GPU; this process enqueues through Python)."""
+    import torch
+
+    iters = min(200, max(10, 20000 // L))
+    for _ in range(3):
+        fn()
+    run = lambda: [fn() for _ in range(iters)]  # noqa: E731
+    return events_ms(cover, run, iters, host_time_ms(run))
 
 
 def copy_reference(a):
@@ -90,17 +167,184 @@ def copy_reference(a):
         for _ in range(a.steps):
             y.copy_(x)
     graph.replay()
-    torch.cuda.synchronize()
-    e0 = torch.cuda.Event(enable_timing=True)
-    e1 = torch.cuda.Event(enable_timing=True)
-    e0.record(torch.cuda.current_stream())
-    graph.replay()
-    e1.record(torch.cuda.current_stream())
-    torch.cuda.synchronize()
-    ms = e0.elapsed_time(e1) / a.steps
+    host = host_time_ms(graph.replay)
+    ms = events_ms(Cover(), graph.replay, a.steps, host)
     gbs = 2 * n * 4 / (ms * 1e-3) / 1e9
     print(json.dumps({"copy_bytes_per_step": 2 * n * 4, "ms_per_step": ms, "GB/s": round(gbs, 1),
                       "frac_of_8TBps": round(gbs / HBM_PEAK_GBS, 4)}), flush=True)
+
+
+def make_workload(sf, torch, dev, B, H, L, io, plan, rotate_mb, seed=0):
+    """Rotated (u, spectrum, y) buffer sets of the benchmark workload, synthetic, in HBM."""
+    import numpy as np
+
+    g = torch.Generator(device=dev).manual_seed(seed)
+    decay = 256.0 if L <= 2048 else 2048.0
+    n = torch.arange(L, device=dev, dtype=torch.float32)
+    s_io = 4 if io == "fp32" else 2
+    set_bytes = B * H * L * 2 * s_io + H * 2 * L * 8
+    # one set already larger than the rotation size defeats the Infinity Cache by itself
+    nsets = 1 if rotate_mb <= 0 or set_bytes > rotate_mb * 1e6 else max(3, int(np.ceil(rotate_mb * 1e6 / set_bytes)))
+    sets = []
+    for i in range(nsets):
+        k = torch.randn(H, L, device=dev, generator=g) * torch.exp(-n / decay) / L ** 0.5
+        u32 = torch.randn(B, H, L, device=dev, generator=g)
+        u = sf.to_bf16(u32) if io == "bf16" else u32
+        kf = sf.spectrum(k, L, plan)
+        y = torch.empty_like(u)
+        sets.append({"u": u, "kf": kf, "y": y, "k": k, "u32": u32 if i == 0 else None})
+    return sets, decay, set_bytes
+
+
+def time_fused(sf, torch, cover, sets, plan, steps, warmup, work=None, warm=True):
+    """ms per step of K graph-replayed steps over the rotated sets; also the same steps
+    launched eagerly, the warm single-set time, and whether the replay reproduced the
+    eager outputs bit for bit."""
+    nsets = len(sets)
+
+    def step(i):
+        s = sets[i % nsets]
+        sf.conv(s["u"], s["kf"], plan, out=s["y"], work=work)
+
+    for i in range(warmup):
+        step(i)
+    for i in range(nsets):  # every buffer set once more, untimed: the eager outputs
+        step(i)
+    torch.cuda.synchronize()
+    y_eager = [s["y"].clone() for s in sets]
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for i in range(steps):
+            step(i)
+    graph.replay()  # untimed replay
+    host = host_time_ms(graph.replay)
+    exact = all(torch.equal(s["y"], y0) for s, y0 in zip(sets, y_eager))
+    ms = events_ms(cover, graph.replay, steps, host)
+    exact = exact and all(torch.equal(s["y"], y0) for s, y0 in zip(sets, y_eager))
+    eager = lambda: [step(i) for i in range(steps)]  # noqa: E731
+    ms_eager = events_ms(cover, eager, steps, host_time_ms(eager))
+    del y_eager
+    ms_warm = None
+    if warm:
+        warm_graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(warm_graph):
+            for i in range(steps):
+                step(0)
+        warm_graph.replay()
+        ms_warm = events_ms(cover, warm_graph.replay, steps, host_time_ms(warm_graph.replay))
+        del warm_graph
+    del graph
+    return ms, ms_eager, ms_warm, exact, step
+
+
+def all_output_error(oracle, np, sets, B, H, L, y=None):
+    """rel-L2 of every B*H*L output against the fp64 oracle (src/sffft.cu:394-399): the
+    direct convolution up to L = 2048, the fp64 FFT convolution beyond it, cross-checked
+    against the direct sum on sequences {0, BH/2, BH-1} (src/sffft.cu:376). The bf16 error
+    includes the I/O rounding: its reference is the fp32 input's."""
+    s0 = sets[0]
+    u_np = s0["u32"].cpu().numpy()
+    k_np = s0["k"].cpu().numpy()
+    if L <= 2048:
+        ref = oracle.direct_conv(u_np, k_np)
+        xcheck = None
+    else:
+        ref = oracle.fft_conv(u_np, k_np)
+        seqs = [0, B * H // 2, B * H - 1]
+        d = oracle.direct_conv_seqs(u_np, k_np, seqs)
+        xcheck = oracle.rel_l2(ref.reshape(B * H, L)[seqs], d)
+    return ref, xcheck
+
+
+def cpu_baseline(oracle, np, u_np, k_np, B, H, L, seconds, cores):
+    """The reference's fp64 direct convolution (src/sffft.cu:377 loop order, the oracle's C
+    restatement) on `cores` host threads: whole-batch passes repeated for about `seconds`
+    when a pass is short, otherwise the first sequences of one pass, scaled to the batch."""
+    t1 = time.perf_counter()
+    oracle.direct_conv(u_np[:1, :1], k_np[:1], nthreads=1)
+    per_seq = max(time.perf_counter() - t1, 1e-6)
+    if per_seq * B * H / cores <= seconds:
+        reps, done = 0, 0.0
+        t1 = time.perf_counter()
+        while done < seconds or reps == 0:
+            oracle.direct_conv(u_np, k_np, nthreads=cores)
+            reps += 1
+            done = time.perf_counter() - t1
+        value = done * 1e3 / reps
+        sample = (f"fp64 direct convolution (src/sffft.cu:377 loop order) of the whole batch "
+                  f"({B * H} sequences at L={L}) repeated {reps} times, {done:.1f} s on {cores} thread(s)")
+    else:
+        nseq = max(cores, int(seconds * cores / per_seq) // cores * cores)
+        us = u_np.reshape(B * H, L)[:nseq].reshape(1, nseq, L)
+        ks = np.stack([k_np[s_ % H] for s_ in range(nseq)])
+        t1 = time.perf_counter()
+        oracle.direct_conv(us, ks, nthreads=cores)
+        done = time.perf_counter() - t1
+        value = done * 1e3 * (B * H) / nseq
+        sample = (f"fp64 direct convolution (src/sffft.cu:377 loop order) of the first {nseq} of {B * H} "
+                  f"sequences at L={L}, {done:.1f} s on {cores} thread(s), scaled linearly to the batch")
+    return {"value": round(value, 3), "unit": "ms per batch", "cores": cores, "kind": "port", "sample": sample}
+
+
+def sweep(a, sf, torch, np, dev, cover):
+    """Every L of the reference table in fp32 and bf16 I/O (src/sffft.cu:506-513,
+    README.md:27-35): graph-timed rotated ms, roofline fraction, all-output rel-L2
+    against fp64, and the reference's own warm protocol for the fused launch and the
+    rocFFT pipeline (fp32, src/sffft.cu:372-381), whose ratio is the speedup."""
+    import oracle
+
+    B, H = a.B, a.H
+    rows = []
+    for L in SWEEP_LENGTHS:
+        ref = xcheck = None
+        rocfft_ms = rocfft_core_ms = rocfft_err = None
+        for io in ("fp32", "bf16"):
+            t0 = time.perf_counter()
+            plan = sf.default_plan(L, io, B)
+            sets, _, set_bytes = make_workload(sf, torch, dev, B, H, L, io, plan, a.rotate_mb)
+            ms, _, ms_warm, exact, step = time_fused(sf, torch, cover, sets, plan, a.steps, 3, warm=True)
+            ms_ref = reference_protocol_ms(cover, lambda: step(0), L)
+            s_io = 4 if io == "fp32" else 2
+            algo = B * H * L * 2 * s_io + H * 2 * L * 8
+            if ref is None:
+                ref, xcheck = all_output_error(oracle, np, sets, B, H, L)
+            step(0)
+            torch.cuda.synchronize()
+            err = oracle.rel_l2(sets[0]["y"].float().cpu().numpy(), ref)
+            if io == "fp32":
+                s0 = sets[0]
+                rp = sf.RocfftPipeline(B, H, L, s0["k"])
+                yr = torch.empty_like(s0["u32"])
+                rocfft_ms = reference_protocol_ms(cover, lambda: rp.full(s0["u32"], yr), L)
+                rocfft_core_ms = reference_protocol_ms(cover, rp.core, L)
+                rp.full(s0["u32"], yr)
+                torch.cuda.synchronize()
+                rocfft_err = oracle.rel_l2(yr.cpu().numpy(), ref)
+                rp.close()
+                del yr
+            row = {"L": L, "io": io, "plan": plan.name(), "waves": plan.waves, "mode": plan.mode,
+                   "channels": plan.channels, "ms": round(ms, 6), "ms_warm": round(ms_warm, 6),
+                   "roofline_frac": round(algo / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                   "rel_l2_vs_fp64": err, "ms_reference_protocol": round(ms_ref, 6),
+                   "rocfft_pipeline_ms": None if rocfft_ms is None else round(rocfft_ms, 6),
+                   "rocfft_core_ms": None if rocfft_core_ms is None else round(rocfft_core_ms, 6),
+                   "rocfft_rel_l2_vs_fp64": rocfft_err,
+                   "speedup_vs_rocfft": None if rocfft_ms is None else round(rocfft_ms / ms_ref, 2),
+                   "graph_replay_bitexact": bool(exact), "rotated_sets": len(sets)}
+            if xcheck is not None:
+                row["oracle_fft_vs_direct"] = xcheck
+            rows.append(row)
+            print(f"# sweep L={L} {io} {plan.name()}: {ms * 1e3:.2f} us frac {row['roofline_frac']} "
+                  f"err {err:.3e} rocfft {rocfft_ms} ({time.perf_counter() - t0:.1f} s)", file=sys.stderr, flush=True)
+            del sets
+            torch.cuda.empty_cache()
+    # the fp32 rocFFT pipeline is the comparator of both I/O rows of a length
+    by_L = {r["L"]: r for r in rows if r["io"] == "fp32"}
+    for r in rows:
+        if r["io"] == "bf16":
+            f = by_L[r["L"]]
+            r["speedup_vs_rocfft"] = round(f["rocfft_pipeline_ms"] / r["ms_reference_protocol"], 2)
+    return rows
 
 
 def main():
@@ -139,23 +383,11 @@ def main():
     if rc:
         raise SystemExit(f"plan {plan!r} unusable for L={L}: {sf.strerror(rc)}")
 
+    t_start = time.perf_counter()
+    cover = Cover()
     # ---- synthetic inputs (the benchmark workload), resident in HBM -------------
-    g = torch.Generator(device=dev).manual_seed(0)
-    decay = 256.0 if L <= 2048 else 2048.0
-    n = torch.arange(L, device=dev, dtype=torch.float32)
+    sets, decay, set_bytes = make_workload(sf, torch, dev, B, H, L, io, plan, a.rotate_mb)
     s_io = 4 if io == "fp32" else 2
-    set_bytes = B * H * L * 2 * s_io + H * 2 * L * 8
-    # one set already larger than the rotation size defeats the Infinity Cache by itself
-    nsets = 1 if a.rotate_mb <= 0 or set_bytes > a.rotate_mb * 1e6 else \
-        max(3, int(np.ceil(a.rotate_mb * 1e6 / set_bytes)))
-    sets = []
-    for i in range(nsets):
-        k = torch.randn(H, L, device=dev, generator=g) * torch.exp(-n / decay) / L ** 0.5
-        u32 = torch.randn(B, H, L, device=dev, generator=g)
-        u = sf.to_bf16(u32) if io == "bf16" else u32
-        kf = sf.spectrum(k, L, plan)
-        y = torch.empty_like(u)
-        sets.append((u, kf, y, k, u32 if i == 0 else None))
     # multi-pass plans: one workspace for every step (the steps run in stream order)
     work = None
     if plan.mode == 2:
@@ -163,56 +395,16 @@ def main():
         work = torch.empty(wb, dtype=torch.uint8, device=dev)
     torch.cuda.synchronize()
 
-    def step(i):
-        u, kf, y = sets[i % nsets][:3]
-        sf.conv(u, kf, plan, out=y, work=work)
-
     # ---- timed region ----------------------------------------------------------
-    # W eager warmup steps; then the K steps are captured once as a HIP graph and
-    # the graph is replayed between two events on the capture-replay stream (what a
-    # production caller does to keep host launch overhead off the GPU timeline).
-    # The same K steps launched eagerly are timed beside it.
-    stream = torch.cuda.current_stream()
-    for i in range(a.warmup):
-        step(i)
-    for i in range(nsets):  # every buffer set once more, untimed: the eager outputs
-        step(i)
-    torch.cuda.synchronize()
-    y_eager = [s_[2].clone() for s_ in sets]
+    # W eager warmup steps; then the K steps are captured once as a HIP graph and the
+    # graph is replayed between two events on the replay stream, behind a spin kernel
+    # that covers the host's enqueue time. The same K steps launched eagerly are timed
+    # beside it, and the same K steps on one buffer set (warm).
+    ms, ms_eager, ms_warm, replay_exact, step = time_fused(sf, torch, cover, sets, plan, a.steps, a.warmup, work)
 
-    def timed(fn, reps):
-        torch.cuda.synchronize()
-        e0 = torch.cuda.Event(enable_timing=True)
-        e1 = torch.cuda.Event(enable_timing=True)
-        t0 = time.perf_counter()
-        e0.record(torch.cuda.current_stream())
-        fn()
-        e1.record(torch.cuda.current_stream())
-        torch.cuda.synchronize()
-        return e0.elapsed_time(e1) / reps, time.perf_counter() - t0
-
-    graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph):
-        for i in range(a.steps):
-            step(i)
-    graph.replay()  # untimed replay
-    torch.cuda.synchronize()
-    replay_exact = all(torch.equal(s_[2], y0) for s_, y0 in zip(sets, y_eager))
-    ms, wall = timed(graph.replay, a.steps)
-    replay_exact = replay_exact and all(torch.equal(s_[2], y0) for s_, y0 in zip(sets, y_eager))
-    ms_eager, _ = timed(lambda: [step(i) for i in range(a.steps)], a.steps)
-
-    # warm (single buffer set, cache-resident for small L) for comparison
-    warm_graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(warm_graph):
-        for i in range(a.steps):
-            step(0)
-    warm_graph.replay()
-    ms_warm, _ = timed(warm_graph.replay, a.steps)
-
-    # dispatch floor: a body-less kernel with the same grid, block and LDS size,
-    # K launches replayed as a graph like the convolution (first call eager: it
-    # sets the kernel's LDS attribute, which is not a stream operation)
+    # dispatch floor: a body-less kernel with the same grid, block and LDS size, K
+    # launches replayed as a graph like the convolution (first call eager: it sets the
+    # kernel's LDS attribute, which is not a stream operation)
     ms_floor = None
     if plan.mode != 2:  # multi-pass steps are three launches of different shapes
         sf.dispatch_floor(B, H, L, plan)
@@ -221,66 +413,47 @@ def main():
             for i in range(a.steps):
                 sf.dispatch_floor(B, H, L, plan)
         floor_graph.replay()
-        ms_floor, _ = timed(floor_graph.replay, a.steps)
+        ms_floor = events_ms(cover, floor_graph.replay, a.steps, host_time_ms(floor_graph.replay))
 
-    # ---- correctness of the measured configuration ----------------------------
-    rel_err = None
+    # ---- correctness of the measured configuration: every output ---------------
+    rel_err = xcheck = None
     if a.check:
         import oracle
 
-        u, kf, y, k, u32 = sets[0]
+        if L <= 16384:
+            ref, xcheck = all_output_error(oracle, np, sets, B, H, L)
+        else:  # multi-pass lengths: the fp64 FFT convolution of 32 sampled sequences
+            idx = np.linspace(0, B * H - 1, 32).astype(np.int64)
+            u_np = sets[0]["u32"].cpu().numpy().reshape(B * H, L)[idx]
+            k_np = sets[0]["k"].cpu().numpy()
+            ref = oracle.fft_conv(u_np[None], np.stack([k_np[int(s) % H] for s in idx]))[0]
         step(0)
         torch.cuda.synchronize()
-        nchk = min(B * H, 96 if L <= 16384 else 32)
-        idx = np.linspace(0, B * H - 1, nchk).astype(np.int64)
-        u_np = u32.cpu().numpy().reshape(B * H, L)[idx]  # fp32 input: bf16 error includes I/O rounding
-        y_np = y.float().cpu().numpy().reshape(B * H, L)[idx]
-        k_np = k.cpu().numpy()
-        ks = np.stack([k_np[int(s) % H] for s in idx])
-        # fp64 direct convolution (the reference's check) up to L = 16384, fp64 FFT beyond
-        ref = (oracle.direct_conv if L <= 16384 else oracle.fft_conv)(u_np[None], ks)[0]
-        rel_err = oracle.rel_l2(y_np, ref)
+        y = sets[0]["y"].float().cpu().numpy()
+        if L > 16384:
+            y = y.reshape(B * H, L)[idx]
+        rel_err = oracle.rel_l2(y, ref)
+        del ref, y
 
     algo_bytes = B * H * L * 2 * s_io + H * 2 * L * 8
     achieved = algo_bytes / (ms * 1e-3) / 1e9
+    u32_np, k_np = sets[0]["u32"].cpu().numpy(), sets[0]["k"].cpu().numpy()
+    nsets, work_bytes = len(sets), None if work is None else work.numel()
+    del sets, work
+    torch.cuda.empty_cache()
+
+    rows = sweep(a, sf, torch, np, dev, cover) if a.sweep and plan.mode != 2 else None
 
     # ---- CPU baseline: the reference's fp64 direct convolution (oracle port) ----
-    # A bounded sample of the same workload: whole-batch passes repeated for about
-    # cpu_seconds when a pass is short, otherwise the first sequences of one pass.
-    cpu = None
+    # A bounded sample of the same workload on all host threads, and on one thread.
+    cpu = cpu1 = None
     if a.cpu_baseline:
         import oracle
 
-        cores = oracle.threads()
-        u, k = sets[0][4], sets[0][3]
-        u_np = u.cpu().numpy()
-        k_np = k.cpu().numpy()
-        t1 = time.perf_counter()
-        oracle.direct_conv(u_np[:1, :1], k_np[:1], nthreads=1)
-        per_seq = max(time.perf_counter() - t1, 1e-6)
-        est_batch = per_seq * B * H / cores
-        if est_batch <= a.cpu_seconds:
-            reps, done = 0, 0.0
-            t1 = time.perf_counter()
-            while done < a.cpu_seconds or reps == 0:
-                oracle.direct_conv(u_np, k_np, nthreads=cores)
-                reps += 1
-                done = time.perf_counter() - t1
-            value = done * 1e3 / reps
-            sample = (f"fp64 direct convolution (src/sffft.cu:377 loop order) of the whole batch "
-                      f"({B * H} sequences at L={L}) repeated {reps} times, {done:.1f} s on {cores} threads")
-        else:
-            nseq = max(cores, int(a.cpu_seconds * cores / per_seq) // cores * cores)
-            us = u_np.reshape(B * H, L)[:nseq].reshape(1, nseq, L)
-            ks = np.stack([k_np[s_ % H] for s_ in range(nseq)])
-            t1 = time.perf_counter()
-            oracle.direct_conv(us, ks, nthreads=cores)
-            done = time.perf_counter() - t1
-            value = done * 1e3 * (B * H) / nseq
-            sample = (f"fp64 direct convolution (src/sffft.cu:377 loop order) of the first {nseq} of {B * H} "
-                      f"sequences at L={L}, {done:.1f} s on {cores} threads, scaled linearly to the batch")
-        cpu = {"value": round(value, 3), "unit": "ms per batch", "cores": cores, "kind": "port", "sample": sample}
+        cpu = cpu_baseline(oracle, np, u32_np, k_np, B, H, L, a.cpu_seconds, oracle.threads())
+        cpu1 = cpu_baseline(oracle, np, u32_np, k_np, B, H, L, a.cpu_seconds, 1)
 
+    stamp = sf.kernel_sources_sha()
     out = {
         "metric": "ms per B=8xH=768 batch vs L (fp32/bf16 I/O); % HBM roofline; rel L2 err",
         "value": round(ms, 6),
@@ -300,21 +473,27 @@ def main():
                             "multi-pass: columns, rows, columns; complex fp16 workspace")[plan.mode],
                    "channels_per_workgroup": plan.channels,
                    "acc": "fp16" if plan.acc else "fp32", "rotated_sets": nsets,
-                   "workspace_bytes": None if work is None else work.numel(),
-                   "rotated_bytes": nsets * set_bytes},
+                   "rotated_bytes": nsets * set_bytes,
+                   "workspace_bytes": work_bytes},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "traffic": profiled_traffic(f"B={B} H={H} L={L} {io}", plan)},
+                     "traffic": profiled_traffic(f"B={B} H={H} L={L} {io}", plan, stamp)},
         "cpu_baseline": cpu,
+        "cpu_baseline_1core": cpu1,
         "ms_warm": round(ms_warm, 6),
         "ms_eager": round(ms_eager, 6),
         "ms_dispatch_floor": None if ms_floor is None else round(ms_floor, 6),
         "io_only_frac": round(B * H * L * 2 * s_io / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
-        "timing": "HIP graph of the K steps replayed between events; ms_eager: the same steps launched one by one",
+        "timing": ("HIP graph of the K steps replayed between events behind a spin kernel that covers the "
+                   "host enqueue; ms_eager: the same steps launched one by one"),
         "graph_replay_bitexact": bool(replay_exact),
         "rel_l2_vs_fp64": rel_err,
+        "rel_l2_outputs": "all B*H*L" if L <= 16384 else "32 sampled sequences",
+        "oracle_fft_vs_direct": xcheck,
         "algorithmic_bytes": algo_bytes,
-        "wall_s": round(wall, 3),
+        "kernel_sources_sha": stamp,
+        "sweep": rows,
+        "wall_s": round(time.perf_counter() - t_start, 1),
     }
     print(json.dumps(out), flush=True)
 

@@ -85,7 +85,10 @@ int sffft_plan_get(int L, int index, sffft_plan* plan, char* name, size_t name_l
 size_t sffft_spectrum_bytes(int H, int L);
 
 /* Filter spectrum in the fused kernel's order, from the real filter k [H][L] fp32.
- * The order depends on the radices and on the mode (mode 0 and mode 1 differ).
+ * The order depends on the radices and on the mode (mode 0 and mode 1 differ). For mode-1
+ * (wave) plans only the Hermitian half is stored (K[2L-f] = conj(K[f]) for a real filter):
+ * (r0/2 + 1) * (8*(r1/16) + 1) * 2 complex64 values per channel, channels consecutive, at
+ * the start of kf; the rest of the sffft_spectrum_bytes buffer is zeroed.
  * `work` must hold sffft_spectrum_bytes(H, L) bytes (scratch, clobbered).
  * Replaces: zero-pad + cufftExecC2C(FORWARD) + permuteK (src/sffft.cu:342-344,365,384,283-288).
  * Arithmetic: fp64 accumulation and twiddles, fp32 storage between the stages. */
@@ -93,11 +96,12 @@ int sffft_spectrum(const float* k, int H, int L, const sffft_plan* plan, void* k
 
 /* Complex input: the spectrum of the complex filter kr + i*ki (kr, ki [H][L] fp32) for a plan
  * with two sequences per transform (seqs = 2; every mode-1 and mode-2 plan). With it,
- * sffft_conv_* and sffft_conv_long_* compute the complex causal convolution
+ * sffft_conv_complex_* (and sffft_conv_long_* for mode-2 plans) compute the complex causal
+ * convolution
  *   y[b] + i y[b+1] = sum_{m<=n} (u[b,m] + i u[b+1,m]) (kr[n-m] + i ki[n-m])
  * for every even b: batch rows 2b' and 2b'+1 of u and y are the real and imaginary planes of
  * complex sequence b'. The reference takes real input only (README.md:174); no counterpart.
- * `work` as in sffft_spectrum; kf holds the sum of both spectra. */
+ * `work` as in sffft_spectrum; kf holds the sum of both spectra, whole (not Hermitian). */
 int sffft_spectrum_complex(const float* kr, const float* ki, int H, int L, const sffft_plan* plan, void* kf,
                            void* work, void* stream);
 
@@ -115,6 +119,14 @@ int sffft_conv_f32(const float* u, const void* kf, float* y, int B, int H, int L
 /* bf16 I/O: u and y hold bf16 bit patterns; y is rounded to nearest even. */
 int sffft_conv_bf16(const uint16_t* u, const void* kf, uint16_t* y, int B, int H, int L,
                     const sffft_plan* plan, void* stream);
+
+/* Complex causal convolution with a spectrum from sffft_spectrum_complex (see there):
+ * seqs = 2 plans of modes 0 and 1, fp32 accumulation; the same launch shape as
+ * sffft_conv_*. No counterpart in the reference (real input only, README.md:174). */
+int sffft_conv_complex_f32(const float* u, const void* kf, float* y, int B, int H, int L,
+                           const sffft_plan* plan, void* stream);
+int sffft_conv_complex_bf16(const uint16_t* u, const void* kf, uint16_t* y, int B, int H, int L,
+                            const sffft_plan* plan, void* stream);
 
 /* Multi-pass convolution (mode-2 plans), for sequences whose length-2L transform does
  * not fit one CU's LDS. No counterpart in the reference, which stops at L = 8192 and

@@ -104,6 +104,8 @@ def lib() -> ctypes.CDLL:
             "sffft_spectrum_from_natural": (ci, [vp, ci, ci, P, vp, vp]),
             "sffft_conv_f32": (ci, [vp, vp, vp, ci, ci, ci, P, vp]),
             "sffft_conv_bf16": (ci, [vp, vp, vp, ci, ci, ci, P, vp]),
+            "sffft_conv_complex_f32": (ci, [vp, vp, vp, ci, ci, ci, P, vp]),
+            "sffft_conv_complex_bf16": (ci, [vp, vp, vp, ci, ci, ci, P, vp]),
             "sffft_work_bytes": (sz, [ci, ci, ci, P]),
             "sffft_conv_long_f32": (ci, [vp, vp, vp, vp, sz, ci, ci, ci, P, vp]),
             "sffft_conv_long_bf16": (ci, [vp, vp, vp, vp, sz, ci, ci, ci, P, vp]),
@@ -337,12 +339,18 @@ def spectrum_complex(k, L: int, plan: Plan, work=None):
 def complex_conv(x, kf, plan: Plan):
     """Complex causal convolution of x [Bc, H, L] complex64 (cuda) with the filters of
     spectrum_complex(): the planes are interleaved as batch rows (2b', 2b'+1) = (Re, Im) of x[b'],
-    convolved with conv(), and reassembled."""
+    convolved by sffft_conv_complex_f32 (conv_long for multi-pass plans), and reassembled."""
     import torch
 
     Bc, H, L = x.shape
     u = torch.stack([x.real, x.imag], 1).reshape(2 * Bc, H, L).contiguous()
-    y = conv(u, kf, plan).reshape(Bc, 2, H, L)
+    if plan.mode == 2:
+        y = conv_long(u, kf, plan)
+    else:
+        y = torch.empty_like(u)
+        _check(lib().sffft_conv_complex_f32(_ptr(u), _ptr(kf), _ptr(y), 2 * Bc, H, L, ctypes.byref(plan),
+                                            _stream()), "sffft_conv_complex_f32")
+    y = y.reshape(Bc, 2, H, L)
     return torch.complex(y[:, 0], y[:, 1])
 
 
@@ -467,6 +475,69 @@ def dft_table():
     buf = (ctypes.c_uint16 * (57344 // 2))()
     _check(lib().sffft_dft_table(buf, 57344), "sffft_dft_table")
     return np.frombuffer(buf, dtype=np.uint16).copy()
+
+
+class RocfftPipeline:
+    """The rocFFT comparator of the driver (libsffft_rocfft.so; the reference's cuFFT
+    pipeline, src/sffft.cu:289-305,365-371): pad -> R2C -> multiply by the half spectrum / N
+    -> C2R -> slice, on the current torch stream. Measurement infrastructure, not part of
+    the drop-in boundary."""
+
+    _rlib = None
+
+    def __init__(self, B: int, H: int, L: int, k):
+        import torch
+
+        if RocfftPipeline._rlib is None:
+            lib()  # binds the HIP runtime torch uses first
+            R = ctypes.CDLL(ROCFFT_LIB_PATH)
+            vp, ci = ctypes.c_void_p, ctypes.c_int
+            R.sffft_rocfft_create.argtypes = [ci, ci, ci, vp, ctypes.POINTER(vp)]
+            R.sffft_rocfft_filter.argtypes = [vp, vp, vp]
+            R.sffft_rocfft_full.argtypes = [vp, vp, vp]
+            R.sffft_rocfft_core.argtypes = [vp]
+            R.sffft_rocfft_destroy.argtypes = [vp]
+            RocfftPipeline._rlib = R
+        self.R = RocfftPipeline._rlib
+        self.h = ctypes.c_void_p()
+        rc = self.R.sffft_rocfft_create(B, H, L, _stream(), ctypes.byref(self.h))
+        if rc:
+            raise RuntimeError(f"sffft_rocfft_create failed ({rc})")
+        assert k.is_cuda and k.dtype == torch.float32 and tuple(k.shape) == (H, L)
+        self.k = k.contiguous()
+        if self.R.sffft_rocfft_filter(self.h, _ptr(self.k), None):
+            raise RuntimeError("sffft_rocfft_filter failed")
+
+    def full(self, u, y) -> None:
+        if self.R.sffft_rocfft_full(self.h, _ptr(u), _ptr(y)):
+            raise RuntimeError("sffft_rocfft_full failed")
+
+    def core(self) -> None:
+        if self.R.sffft_rocfft_core(self.h):
+            raise RuntimeError("sffft_rocfft_core failed")
+
+    def close(self) -> None:
+        if self.h:
+            self.R.sffft_rocfft_destroy(self.h)
+            self.h = ctypes.c_void_p()
+
+
+# Sources that determine the kernels' machine code: a profile summary measured on a
+# build of other sources does not describe this one.
+KERNEL_SOURCES = ("csrc/fftconv.hpp", "csrc/fftconv_wave.hpp", "csrc/longconv.hpp", "csrc/transforms.hpp",
+                  "csrc/registry.hpp", "csrc/plans.def", "csrc/conv_inst.hip", "csrc/long_inst.hip", "csrc/api.hip",
+                  "Makefile")
+
+
+def kernel_sources_sha() -> str:
+    """First 16 hex digits of the sha256 over the kernel sources and build flags."""
+    import hashlib
+
+    h = hashlib.sha256()
+    for rel in KERNEL_SOURCES:
+        with open(os.path.join(_HERE, rel), "rb") as f:
+            h.update(rel.encode() + b"\0" + f.read() + b"\0")
+    return h.hexdigest()[:16]
 
 
 def loaded_library_paths() -> List[str]:

@@ -53,11 +53,13 @@ size_t lds_bytes_rt(int r0, int r1, int r2, int mode, int channels, int waves) {
   if (mode == 1) {
     // WavePlan::lds_bytes: the twiddle tables (one when r0 == r1), the row-load scratch and,
     // in order of preference, both DFT fragment kinds and the spectra; the first kind only
-    // and the spectra; or the first kind only (spectra read through L2)
+    // and the spectra; or the first kind only (spectra read through L2). The spectra are
+    // Hermitian halves (WavePlan::HSP_F4 float4 per channel) in whole 64-float4 runs.
     const int T0 = r0 / 16, T1 = r1 / 16, N = r0 * r1;
     const size_t frags = (size_t)(T0 * T0 * 128 + (r1 == r0 ? 0 : T1 * T1 * 128)) * 16;
     const size_t tw = (size_t)((r1 == r0 ? 1 : 2) * N / 2) * 16;
-    const size_t scratch = (size_t)waves * 16 * (r1 + 4) * 4, spectra = (size_t)channels * N / 2 * 16;
+    const size_t half_f4 = (size_t)(r0 / 2 + 1) * (8 * T1 + 1);
+    const size_t scratch = (size_t)waves * 16 * (r1 + 4) * 4, spectra = (channels * half_f4 + 63) / 64 * 64 * 16;
     const size_t tab = frags + tw + spectra + scratch <= 163840 ? frags + tw : frags / 2 + tw;
     const bool in_lds = tab + spectra + scratch <= 163840;
     return tab + (in_lds ? spectra : 0) + scratch;
@@ -361,6 +363,37 @@ __global__ void spectrum_permute_kernel(const float2* __restrict__ src, float2* 
   }
 }
 
+// Hermitian half of a real filter's spectrum in the wave pipeline's order
+// (WavePlan::hs_index): per channel, (r0/2 + 1) columns k0 of PITCH = 8*(r1/16) + 1
+// float4; float4 (k0*PITCH + (kt*2 + q)*4 + g) holds k1 = 16kt + 4g + 2q and +1, i.e.
+// K[k0 + r0*k1]. Column r0/2 holds conj(K[r0/2 + r0*(r1 - 1 - k1)]) at k1; the last float4
+// of each column is zero padding. src as in spectrum_permute_kernel; channels are
+// consecutive (2*(r0/2 + 1)*PITCH complex values each), and the rest of the H*N buffer
+// is zeroed, so the whole buffer is a function of the filter.
+__global__ void spectrum_half_kernel(const float2* __restrict__ src, float2* __restrict__ kf, int H, int r0, int r1,
+                                     int natural, float scale) {
+  const int pitch = 8 * (r1 / 16) + 1, C = 2 * (r0 / 2 + 1) * pitch, N = r0 * r1;
+  const size_t gid = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (gid >= (size_t)H * N) return;
+  if (gid >= (size_t)H * C) {
+    kf[gid] = make_float2(0.f, 0.f);
+    return;
+  }
+  const int h = (int)(gid / C), i = (int)(gid % C);
+  const int f = i >> 1, e = i & 1, k0 = f / pitch, rem = f % pitch;
+  if (rem == pitch - 1) {
+    kf[gid] = make_float2(0.f, 0.f);
+    return;
+  }
+  const int g = rem & 3, q = (rem >> 2) & 1, kt = rem >> 3;
+  const int k1 = 16 * kt + 4 * g + 2 * q + e;
+  const bool mid = k0 == r0 / 2;
+  const int kk1 = mid ? r1 - 1 - k1 : k1;
+  const int sidx = natural ? k0 + r0 * kk1 : k0 * r1 + kk1;
+  const float2 v = src[(size_t)h * N + sidx];
+  kf[gid] = make_float2(v.x * scale, (mid ? -v.y : v.y) * scale);
+}
+
 __global__ void to_bf16_kernel(const float* __restrict__ x, uint16_t* __restrict__ y, size_t n) {
   const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i < n) y[i] = f32_to_bf16(x[i]);
@@ -383,8 +416,11 @@ bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 // launch and retirement) without any memory traffic.
 __global__ void empty_dispatch_kernel() {}
 
+// cplx: complex filters (whole spectra from sffft_spectrum_complex); wave plans then run
+// their non-Hermitian instantiation, the other plans read whole spectra anyway.
 template <int IO>
-int conv(const void* u, const void* kf, void* y, int B, int H, int L, const sffft_plan* p, void* stream) {
+int conv(const void* u, const void* kf, void* y, int B, int H, int L, const sffft_plan* p, void* stream,
+         int cplx = 0) {
   if (!u || !kf || !y || B < 1 || H < 1 || (long long)B * H > INT_MAX) return SFFFT_EINVAL;
   int rc = check_shape(L, p);
   if (rc) return rc;
@@ -397,8 +433,8 @@ int conv(const void* u, const void* kf, void* y, int B, int H, int L, const sfff
   if ((rc = device_table(&table))) return rc;
   const void* tw = nullptr;
   if (e->mode == 1 && (rc = device_twiddles(p->r0, p->r1, &tw))) return rc;
-  return hip_status(e->launch[IO][p->cached](u, kf, y, B, H, table, tw, p->acc, (hipStream_t)stream),
-                    "fused convolution launch");
+  const launch_fn fn = cplx && e->mode == 1 ? e->launch_complex[IO][p->cached] : e->launch[IO][p->cached];
+  return hip_status(fn(u, kf, y, B, H, table, tw, p->acc, (hipStream_t)stream), "fused convolution launch");
 }
 
 // Workspace of one channel (its B/2 pairs of 2L complex fp16 points); a workspace of
@@ -462,8 +498,25 @@ int long_plans_for(int L, const LongEntry** out, int cap) {
 }
 
 // imag: k is the imaginary part of a complex filter; its spectrum is added times i to kf
+// Launches the gather of a p-order (natural = 0) or natural-order spectrum into the
+// kernel order of the plan: the Hermitian half for wave plans (mode 1) unless `whole`
+// (complex filters), else the whole spectrum.
+int permute_launch(const float2* src, float2* kf, int H, const sffft_plan* plan, int natural, int imag, int whole,
+                   hipStream_t s) {
+  if (plan->mode == 1 && !whole) {
+    const size_t total = (size_t)H * plan->r0 * plan->r1;
+    hipLaunchKernelGGL(spectrum_half_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, src, kf, H,
+                       plan->r0, plan->r1, natural, last_stage_scale(plan));
+  } else {
+    const size_t total = (size_t)H * plan->r0 * plan->r1 * plan->r2;
+    hipLaunchKernelGGL(spectrum_permute_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, src, kf, H,
+                       plan->r0, plan->r1, plan->r2, plan->mode, natural, last_stage_scale(plan), imag);
+  }
+  return hip_status(hipGetLastError(), "spectrum permute launch");
+}
+
 int spectrum_impl(const float* k, int H, int L, int klen, const sffft_plan* plan, void* kf, void* work,
-                  void* stream, int imag = 0) {
+                  void* stream, int imag = 0, int whole = 0) {
   if (!k || !kf || !work || H < 1 || kf == work) return SFFFT_EINVAL;
   const int rc = check_shape(L, plan);
   if (rc) return rc;
@@ -478,11 +531,7 @@ int spectrum_impl(const float* k, int H, int L, int klen, const sffft_plan* plan
     const int st = hip_status(hipGetLastError(), "spectrum stage launch");
     if (st) return st;
   }
-  const size_t total = (size_t)H * N;
-  hipLaunchKernelGGL(spectrum_permute_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s,
-                     (const float2*)w, static_cast<float2*>(kf), H, plan->r0, plan->r1, plan->r2, plan->mode, 0,
-                     last_stage_scale(plan), imag);
-  return hip_status(hipGetLastError(), "spectrum permute launch");
+  return permute_launch(w, static_cast<float2*>(kf), H, plan, 0, imag, whole, s);
 }
 }  // namespace
 }  // namespace sffft
@@ -570,8 +619,8 @@ int sffft_spectrum_complex(const float* kr, const float* ki, int H, int L, const
                            void* work, void* stream) {
   // pairs of sequences per transform only: they carry the real and imaginary planes of u and y
   if (!plan || plan->seqs != 2 || !ki || ki == kr) return SFFFT_EINVAL;
-  const int rc = spectrum_impl(kr, H, L, L, plan, kf, work, stream);
-  return rc ? rc : spectrum_impl(ki, H, L, L, plan, kf, work, stream, 1);
+  const int rc = spectrum_impl(kr, H, L, L, plan, kf, work, stream, 0, 1);
+  return rc ? rc : spectrum_impl(ki, H, L, L, plan, kf, work, stream, 1, 1);
 }
 
 int sffft_spectrum_circular(const float* k, int H, int N, const sffft_plan* plan, void* kf, void* work,
@@ -596,11 +645,8 @@ int sffft_spectrum_from_natural(const void* kc, int H, int L, const sffft_plan* 
   if (!kc || !kf || H < 1 || kc == kf) return SFFFT_EINVAL;
   const int rc = check_shape(L, plan);
   if (rc) return rc;
-  const size_t total = (size_t)H * 2 * L;
-  hipLaunchKernelGGL(spectrum_permute_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0,
-                     (hipStream_t)stream, static_cast<const float2*>(kc), static_cast<float2*>(kf), H, plan->r0,
-                     plan->r1, plan->r2, plan->mode, 1, last_stage_scale(plan));
-  return hip_status(hipGetLastError(), "spectrum permute launch");
+  return permute_launch(static_cast<const float2*>(kc), static_cast<float2*>(kf), H, plan, 1, 0, 0,
+                        (hipStream_t)stream);
 }
 
 int sffft_conv_f32(const float* u, const void* kf, float* y, int B, int H, int L, const sffft_plan* plan,
@@ -611,6 +657,18 @@ int sffft_conv_f32(const float* u, const void* kf, float* y, int B, int H, int L
 int sffft_conv_bf16(const uint16_t* u, const void* kf, uint16_t* y, int B, int H, int L, const sffft_plan* plan,
                     void* stream) {
   return conv<1>(u, kf, y, B, H, L, plan, stream);
+}
+
+int sffft_conv_complex_f32(const float* u, const void* kf, float* y, int B, int H, int L, const sffft_plan* plan,
+                           void* stream) {
+  if (!plan || plan->seqs != 2 || plan->acc != 0 || plan->mode == 2) return SFFFT_EINVAL;
+  return conv<0>(u, kf, y, B, H, L, plan, stream, 1);
+}
+
+int sffft_conv_complex_bf16(const uint16_t* u, const void* kf, uint16_t* y, int B, int H, int L,
+                            const sffft_plan* plan, void* stream) {
+  if (!plan || plan->seqs != 2 || plan->acc != 0 || plan->mode == 2) return SFFFT_EINVAL;
+  return conv<1>(u, kf, y, B, H, L, plan, stream, 1);
 }
 
 size_t sffft_work_bytes(int B, int H, int L, const sffft_plan* plan) {
@@ -657,11 +715,16 @@ bool span_overlap(const void* a, size_t na, const void* b, size_t nb) {
 }
 bool aligned8(const void* p) { return ((uintptr_t)p & 7u) == 0; }
 
-// Validated 1-D transform layout; *elems: extent of x / X in complex elements.
+// Validated 1-D transform layout; *extent: extent of x / X in complex elements. The layout
+// must be one-to-one (no two (sequence, element) pairs at one address): each sequence
+// whole before the next (dist >= N * stride), or the sequences interleaved within one
+// element step (stride >= batch * dist), as the columns of a row-major matrix are.
 int fft_layout(int batch, int N, long long stride, long long dist, xf::Seqs* q, long long* extent) {
   xf::Radices d;
   if (batch < 1 || !xf::split(N, &d) || (long long)batch * N > xf::MAX_ELEMS) return SFFFT_EINVAL;
   if (stride < 1 || dist < 0 || (batch > 1 && dist < 1)) return SFFFT_EINVAL;
+  if (batch > 1 && stride > ((long long)1 << 40) / N) return SFFFT_EINVAL;  // keeps N * stride in range
+  if (batch > 1 && dist < (long long)N * stride && stride < (long long)batch * dist) return SFFFT_EINVAL;
   *q = xf::Seqs{batch, batch, dist, 0, stride, dist < stride ? 1 : 0};
   *extent = (long long)(batch - 1) * dist + (long long)(N - 1) * stride + 1;
   return SFFFT_OK;
@@ -701,6 +764,9 @@ int sffft_fft_c2c(const void* x, void* X, void* work, size_t work_bytes, int bat
   long long ext;
   if (!x || !X || !aligned8(x) || !aligned8(X) || (inverse != 0 && inverse != 1)) return SFFFT_EINVAL;
   if (fft_layout(batch, N, stride, dist, &q, &ext)) return SFFFT_EINVAL;
+  // in place (x == X) or disjoint; a partial overlap would let one stage overwrite input
+  // another thread has yet to read
+  if (x != X && span_overlap(x, (size_t)ext * 8, X, (size_t)ext * 8)) return SFFFT_EINVAL;
   const size_t need = (size_t)xf::work_elems(q, N) * 8;
   if (need && (!work || !aligned8(work) || work_bytes < need || span_overlap(work, need, x, ext * 8) ||
                span_overlap(work, need, X, ext * 8)))

@@ -25,13 +25,24 @@ static hipError_t launch_wave(const void* u, const void* kf, void* y, int B, int
                               const void* tw, int acc16, hipStream_t stream) {
   const unsigned grid = (unsigned)((H + CH - 1) / CH);
   if (acc16)
-    hipLaunchKernelGGL((fftconv_wave_kernel<P, NW, CH, TIO, CACHED, true>), dim3(grid), dim3(64 * NW), 0, stream,
-                       static_cast<const TIO*>(u), static_cast<const float4*>(kf), static_cast<TIO*>(y), B, H,
-                       static_cast<const h8*>(ftab), static_cast<const float4*>(tw));
+    hipLaunchKernelGGL((fftconv_wave_kernel<P, NW, CH, TIO, CACHED, true, true>), dim3(grid), dim3(64 * NW), 0,
+                       stream, static_cast<const TIO*>(u), static_cast<const float4*>(kf), static_cast<TIO*>(y), B,
+                       H, static_cast<const h8*>(ftab), static_cast<const float4*>(tw));
   else
-    hipLaunchKernelGGL((fftconv_wave_kernel<P, NW, CH, TIO, CACHED, false>), dim3(grid), dim3(64 * NW), 0, stream,
-                       static_cast<const TIO*>(u), static_cast<const float4*>(kf), static_cast<TIO*>(y), B, H,
-                       static_cast<const h8*>(ftab), static_cast<const float4*>(tw));
+    hipLaunchKernelGGL((fftconv_wave_kernel<P, NW, CH, TIO, CACHED, false, true>), dim3(grid), dim3(64 * NW), 0,
+                       stream, static_cast<const TIO*>(u), static_cast<const float4*>(kf), static_cast<TIO*>(y), B,
+                       H, static_cast<const h8*>(ftab), static_cast<const float4*>(tw));
+  return hipGetLastError();
+}
+
+// complex filters: whole spectra, fp32 accumulation
+template <class P, int NW, int CH, class TIO, bool CACHED>
+static hipError_t launch_wave_complex(const void* u, const void* kf, void* y, int B, int H, const void* ftab,
+                                      const void* tw, int, hipStream_t stream) {
+  const unsigned grid = (unsigned)((H + CH - 1) / CH);
+  hipLaunchKernelGGL((fftconv_wave_kernel<P, NW, CH, TIO, CACHED, false, false>), dim3(grid), dim3(64 * NW), 0,
+                     stream, static_cast<const TIO*>(u), static_cast<const float4*>(kf), static_cast<TIO*>(y), B, H,
+                     static_cast<const h8*>(ftab), static_cast<const float4*>(tw));
   return hipGetLastError();
 }
 
@@ -44,7 +55,8 @@ static Entry make_entry() {
              {{reinterpret_cast<const void*>(&fftconv_kernel<P, W, S, float, false>),
                reinterpret_cast<const void*>(&fftconv_kernel<P, W, S, float, true>)},
               {reinterpret_cast<const void*>(&fftconv_kernel<P, W, S, uint16_t, false>),
-               reinterpret_cast<const void*>(&fftconv_kernel<P, W, S, uint16_t, true>)}}};
+               reinterpret_cast<const void*>(&fftconv_kernel<P, W, S, uint16_t, true>)}},
+             {{nullptr, nullptr}, {nullptr, nullptr}}};
   return e;
 }
 
@@ -54,10 +66,12 @@ static Entry make_wave_entry() {
   Entry e = {SFFFT_INST_L, A, B_, 1, W, 2, 1, CH, P::lds_bytes(CH, W),
              {{&launch_wave<P, W, CH, float, false>, &launch_wave<P, W, CH, float, true>},
               {&launch_wave<P, W, CH, uint16_t, false>, &launch_wave<P, W, CH, uint16_t, true>}},
-             {{reinterpret_cast<const void*>(&fftconv_wave_kernel<P, W, CH, float, false, false>),
-               reinterpret_cast<const void*>(&fftconv_wave_kernel<P, W, CH, float, true, false>)},
-              {reinterpret_cast<const void*>(&fftconv_wave_kernel<P, W, CH, uint16_t, false, false>),
-               reinterpret_cast<const void*>(&fftconv_wave_kernel<P, W, CH, uint16_t, true, false>)}}};
+             {{reinterpret_cast<const void*>(&fftconv_wave_kernel<P, W, CH, float, false, false, true>),
+               reinterpret_cast<const void*>(&fftconv_wave_kernel<P, W, CH, float, true, false, true>)},
+              {reinterpret_cast<const void*>(&fftconv_wave_kernel<P, W, CH, uint16_t, false, false, true>),
+               reinterpret_cast<const void*>(&fftconv_wave_kernel<P, W, CH, uint16_t, true, false, true>)}},
+             {{&launch_wave_complex<P, W, CH, float, false>, &launch_wave_complex<P, W, CH, float, true>},
+              {&launch_wave_complex<P, W, CH, uint16_t, false>, &launch_wave_complex<P, W, CH, uint16_t, true>}}};
   return e;
 }
 

@@ -36,7 +36,11 @@
 // indices, so TW2 is TW1 and the spectrum carries sc1 as well (1/R1).
 // The channel spectra sit in LDS when they fit beside the tables and the operand
 // scratch; otherwise the wavefronts read them from global memory (L2-resident:
-// B/2 wavefronts read each channel's spectrum).
+// B/2 wavefronts read each channel's spectrum). A real filter's spectrum is
+// Hermitian, K[N-k] = conj(K[k]), so only its columns k0 = 0..R0/2 are stored (about
+// half the bytes, WavePlan::hs_index) and the lanes of columns k0 > R0/2 read the
+// partner frequency N-k and conjugate it; complex filters (HERM = false) read the
+// whole spectrum.
 #pragma once
 #include "fftconv.hpp"
 
@@ -54,7 +58,15 @@ struct WavePlan {
   static constexpr int F0_H8 = ST * ST * 128;  // both fragment kinds
   static constexpr int F1_H8 = R1 == R0 ? 0 : MT * MT * 128;
   static constexpr int TW_F4 = N / 2;  // one twiddle table: N complex fp32 = N/2 float4
-  static constexpr int SP_F4 = N / 2;  // one channel's spectrum: N complex64 = N/2 float4
+  static constexpr int SP_F4 = N / 2;  // one channel's whole spectrum: N complex64 = N/2 float4
+  // One channel's Hermitian half spectrum (hs_index): columns k0 = 0..R0/2 of HPITCH
+  // float4 each (8*MT values and one of padding: an odd pitch puts the 16 columns a
+  // lane group reads on 16 distinct 16-byte slots).
+  static constexpr int HPITCH = 8 * MT + 1;
+  static constexpr int HSP_F4 = (R0 / 2 + 1) * HPITCH;
+  static constexpr int sp_f4(bool herm) { return herm ? HSP_F4 : SP_F4; }
+  // ch channels' spectra in LDS, in whole 64-float4 runs of the table copy
+  static constexpr int spl_f4(int ch, bool herm) { return (ch * sp_f4(herm) + 63) / 64 * 64; }
   static constexpr int TW_TABLES = R0 == R1 ? 1 : 2;
   static constexpr int TAB_F4 = F0_H8 + F1_H8 + TW_TABLES * TW_F4;
   // the same with the first fragment kind only (the second is derived in registers)
@@ -65,15 +77,18 @@ struct WavePlan {
   // both DFT fragment kinds and the spectra in LDS; the first kind only with the spectra
   // in LDS; the first kind only with the spectra read through L2. Every layout reads the
   // pairs as row chunks through the operand scratch.
-  static constexpr bool both_kinds(int ch, int nw) {
-    return (TAB_F4 + ch * SP_F4) * 16 + nw * SCRATCH_MAX <= 163840;
+  static constexpr bool both_kinds(int ch, int nw, bool herm = true) {
+    return (TAB_F4 + spl_f4(ch, herm)) * 16 + nw * SCRATCH_MAX <= 163840;
   }
-  static constexpr int tables_f4(int ch, int nw) { return both_kinds(ch, nw) ? TAB_F4 : TAB1_F4; }
-  static constexpr bool spectra_in_lds(int ch, int nw) {
-    return (tables_f4(ch, nw) + ch * SP_F4) * 16 + nw * SCRATCH_MAX <= 163840;
+  static constexpr int tables_f4(int ch, int nw, bool herm = true) {
+    return both_kinds(ch, nw, herm) ? TAB_F4 : TAB1_F4;
   }
-  static constexpr int lds_bytes(int ch, int nw) {
-    return (tables_f4(ch, nw) + (spectra_in_lds(ch, nw) ? ch * SP_F4 : 0)) * 16 + nw * SCRATCH_MAX;
+  static constexpr bool spectra_in_lds(int ch, int nw, bool herm = true) {
+    return (tables_f4(ch, nw, herm) + spl_f4(ch, herm)) * 16 + nw * SCRATCH_MAX <= 163840;
+  }
+  static constexpr int lds_bytes(int ch, int nw, bool herm = true) {
+    return (tables_f4(ch, nw, herm) + (spectra_in_lds(ch, nw, herm) ? spl_f4(ch, herm) : 0)) * 16 +
+           nw * SCRATCH_MAX;
   }
   static_assert(R0 >= 16 && R0 <= 64 && R1 >= 16 && R1 <= 64, "radices are 16, 32 or 64");
 };
@@ -83,6 +98,14 @@ __host__ __device__ constexpr int tw_index(int tile, int lane, int q) { return (
 // Spectrum index (float4 units) in the wave pipeline's order: tile = s*MT + kt,
 // q as above; lanes at 16-byte stride so one load instruction reads 1 KB.
 __host__ __device__ constexpr int sp_index(int tile, int lane, int q) { return (tile * 2 + q) * 64 + lane; }
+// Hermitian half spectrum (float4 units): the float4 at hs_index(k0, kt, q, g) holds the
+// values k1 = 16kt + 4g + 2q and +1 of column k0 <= R0/2, i.e. K[k0 + R0*k1]. Column
+// R0/2 is stored in the form its own lanes read it as a partner (see herm_spectrum_pack):
+// conj(K[R0/2 + R0*(R1 - 1 - k1)]) at k1.
+template <class P>
+__host__ __device__ constexpr int hs_index(int k0, int kt, int q, int g) {
+  return k0 * P::HPITCH + (kt * 2 + q) * 4 + g;
+}
 
 // DFT fragment (a, b, kind) of a radix-R table in LDS: coefficient-table order, or
 // with K1 the first kind [cos | sin] only. The second kind [-sin | cos] is then the
@@ -114,17 +137,53 @@ __device__ __forceinline__ h8 cmul_pack(f4 dr, f4 di, float4 w01, float4 w23) {
   return o;
 }
 
-// conj((dr + i di) * k) for four spectrum values k (float4 pairs of complex64).
+// conj((dr + i di) * k) for four spectrum values k (float4 pairs of complex64); with
+// CONJ the values given are conj(k) (the signs of the products absorb the conjugation).
+template <bool CONJ = false>
 __device__ __forceinline__ h8 spectrum_conj_pack(f4 dr, f4 di, float4 k01, float4 k23) {
   const float kr[4] = {k01.x, k01.z, k23.x, k23.z};
   const float ki[4] = {k01.y, k01.w, k23.y, k23.w};
   h8 o;
 #pragma unroll
   for (int v = 0; v < 4; v++) {
-    o[v] = (_Float16)(dr[v] * kr[v] - di[v] * ki[v]);
-    o[4 + v] = (_Float16)(-(dr[v] * ki[v] + di[v] * kr[v]));
+    if constexpr (CONJ) {
+      o[v] = (_Float16)(dr[v] * kr[v] + di[v] * ki[v]);
+      o[4 + v] = (_Float16)(dr[v] * ki[v] - di[v] * kr[v]);
+    } else {
+      o[v] = (_Float16)(dr[v] * kr[v] - di[v] * ki[v]);
+      o[4 + v] = (_Float16)(-(dr[v] * ki[v] + di[v] * kr[v]));
+    }
   }
   return o;
+}
+
+// conj(D * K) for lane (j, g) of the phase-2 tile of strip s and k1 tile kt, from a
+// Hermitian half spectrum: K at k0 = 16s + j and k1 = 16kt + 4g + v, v = 0..3. Columns
+// k0 < R0/2 are read directly. A column k0 >= R0/2 holds conj(K) of the partner
+// frequency N - k: column R0 - k0 and k1' = R1 - 1 - k1, so the lane reads tile
+// MT-1-kt, lane group 3-g and the other float4 of its pair, in reverse value order.
+// For R0 >= 32 a strip is wholly direct or wholly partner (no per-lane choice); with
+// R0 = 16 the single strip splits at lane j = 8.
+template <class P>
+__device__ __forceinline__ h8 herm_spectrum_pack(f4 dr, f4 di, const float4* SP, int s, int kt, int lane) {
+  constexpr int R0 = P::R0, MT = P::MT;
+  const int j = lane & 15, g = lane >> 4;
+  const int dk0 = 16 * s + j, pk0 = R0 - 16 * s - j;
+  if (16 * s + 15 < R0 / 2) {
+    return spectrum_conj_pack<false>(dr, di, SP[hs_index<P>(dk0, kt, 0, g)], SP[hs_index<P>(dk0, kt, 1, g)]);
+  } else if (16 * s >= R0 / 2) {
+    // p0: conj(K) of v = 1, 0; p1: of v = 3, 2
+    const float4 p0 = SP[hs_index<P>(pk0, MT - 1 - kt, 1, 3 - g)];
+    const float4 p1 = SP[hs_index<P>(pk0, MT - 1 - kt, 0, 3 - g)];
+    return spectrum_conj_pack<true>(dr, di, make_float4(p0.z, p0.w, p0.x, p0.y), make_float4(p1.z, p1.w, p1.x, p1.y));
+  } else {
+    const bool dir = dk0 < R0 / 2;
+    const float4 a0 = SP[dir ? hs_index<P>(dk0, kt, 0, g) : hs_index<P>(pk0, MT - 1 - kt, 1, 3 - g)];
+    const float4 a1 = SP[dir ? hs_index<P>(dk0, kt, 1, g) : hs_index<P>(pk0, MT - 1 - kt, 0, 3 - g)];
+    const float4 k01 = dir ? a0 : make_float4(a0.z, -a0.w, a0.x, -a0.y);
+    const float4 k23 = dir ? a1 : make_float4(a1.z, -a1.w, a1.x, -a1.y);
+    return spectrum_conj_pack<false>(dr, di, k01, k23);
+  }
 }
 
 template <bool ACC16>
@@ -304,7 +363,7 @@ __device__ __forceinline__ void store_rows(TIO* S, const f4 (&z)[P::MT], TIO* __
 
 // Every stage of one pair, from its loaded operands to the stored outputs; SP is the
 // channel's spectrum in LDS.
-template <class P, class TIO, bool ACC16, bool HOLD_F1, bool K1>
+template <class P, class TIO, bool ACC16, bool HOLD_F1, bool K1, bool HERM>
 __device__ __forceinline__ void process_pair(const PairLoads<P, TIO>& d, TIO* S, const float4* SP,
                                              TIO* __restrict__ ya, TIO* __restrict__ yb, const h8* F0,
                                              const h8* F1, const float4* TW1, const float4* TW2, int lane) {
@@ -374,7 +433,10 @@ __device__ __forceinline__ void process_pair(const PairLoads<P, TIO>& d, TIO* S,
       dr = acc_round<ACC16>(dr);
       di = acc_round<ACC16>(di);
       const int tile = s * MT + kt;
-      a2[kt] = spectrum_conj_pack(dr, di, SP[sp_index(tile, lane, 0)], SP[sp_index(tile, lane, 1)]);
+      if constexpr (HERM)
+        a2[kt] = herm_spectrum_pack<P>(dr, di, SP, s, kt, lane);
+      else
+        a2[kt] = spectrum_conj_pack(dr, di, SP[sp_index(tile, lane, 0)], SP[sp_index(tile, lane, 1)]);
     }
 #pragma unroll
     for (int t = 0; t < MT; t++) {
@@ -423,17 +485,20 @@ __device__ __forceinline__ void process_pair(const PairLoads<P, TIO>& d, TIO* S,
 // and (2bp+1, h), h = w*CH + c. Wave v takes pairs v, v + NW, ... The DFT and
 // twiddle tables and the CH channel spectra are copied into LDS once, so the
 // B/2 wavefronts of a channel read its spectrum from LDS rather than each from L2.
-template <class P, int NW, int CH, class TIO, bool CACHED, bool ACC16>
+// HERM: kf holds Hermitian half spectra (real filters, hs_index, HSP_F4 float4 per
+// channel); otherwise whole spectra (complex filters, sp_index, SP_F4 per channel).
+template <class P, int NW, int CH, class TIO, bool CACHED, bool ACC16, bool HERM>
 __global__ void __launch_bounds__(64 * NW)
     fftconv_wave_kernel(const TIO* __restrict__ u, const float4* __restrict__ kf, TIO* __restrict__ y, int B,
                         int H, const h8* __restrict__ ftab, const float4* __restrict__ twtab) {
   constexpr int R0 = P::R0;
-  constexpr bool K1 = !P::both_kinds(CH, NW);  // first DFT fragment kind only
+  constexpr bool K1 = !P::both_kinds(CH, NW, HERM);  // first DFT fragment kind only
   constexpr int SCR_F4 = scratch_bytes<P, TIO>() / 16;
-  constexpr bool SP_LDS = P::spectra_in_lds(CH, NW);
-  constexpr int SPL_F4 = SP_LDS ? CH * P::SP_F4 : 0, TAB_F4 = P::tables_f4(CH, NW);
+  constexpr bool SP_LDS = P::spectra_in_lds(CH, NW, HERM);
+  constexpr int SPC_F4 = P::sp_f4(HERM);  // one channel's spectrum
+  constexpr int SPL_F4 = SP_LDS ? P::spl_f4(CH, HERM) : 0, TAB_F4 = P::tables_f4(CH, NW, HERM);
   constexpr int F0_H8 = K1 ? P::F0_H8 / 2 : P::F0_H8, F1_H8 = K1 ? P::F1_H8 / 2 : P::F1_H8;
-  static_assert((TAB_F4 + SPL_F4 + NW * SCR_F4) * 16 <= P::lds_bytes(CH, NW), "layout within the plan's LDS");
+  static_assert((TAB_F4 + SPL_F4 + NW * SCR_F4) * 16 <= P::lds_bytes(CH, NW, HERM), "layout within the plan's LDS");
   __shared__ float4 lds[TAB_F4 + SPL_F4 + NW * SCR_F4];
   h8* F0 = reinterpret_cast<h8*>(lds);
   h8* F1 = P::R1 == P::R0 ? F0 : F0 + F0_H8;
@@ -460,16 +525,17 @@ __global__ void __launch_bounds__(64 * NW)
       dma_to_lds<F1_H8, NW>(reinterpret_cast<float4*>(F1), [&](int k) { return tab(P::R1, k); }, lane, wave);
   }
   if constexpr (SP_LDS) {
-    // channel c of this workgroup is in slot c; slots past the last channel copy
-    // the last channel again (in bounds, never read)
-    const float4* src = kf + (size_t)h0 * P::SP_F4;
-    const int last = nch * P::SP_F4 - 1;
-    dma_to_lds<CH * P::SP_F4, NW>(SPL, [&](int k) { return src + (k < last ? k : last); }, lane, wave);
+    // channel c of this workgroup is in slot c (the channels' spectra are consecutive in
+    // global memory); what the copy's whole runs add past the last channel repeats the
+    // last float4 of the last channel (in bounds, never read)
+    const float4* src = kf + (size_t)h0 * SPC_F4;
+    const int last = nch * SPC_F4 - 1;
+    dma_to_lds<SPL_F4, NW>(SPL, [&](int k) { return src + (k < last ? k : last); }, lane, wave);
   }
   // spectrum of channel slot c: in LDS, or the channel's row in global memory
   auto spec = [&](int c) -> const float4* {
-    if constexpr (SP_LDS) return SPL + c * P::SP_F4;
-    else return kf + (size_t)(h0 + c) * P::SP_F4;
+    if constexpr (SP_LDS) return SPL + c * SPC_F4;
+    else return kf + (size_t)(h0 + c) * SPC_F4;
   };
   if constexpr (!CACHED) {
     compute_dft<R0, 64 * NW, K1>(F0, tid);
@@ -510,7 +576,7 @@ __global__ void __launch_bounds__(64 * NW)
   if (wave < npairs) {
     const int c = wave / BP, bp = wave - c * BP;
     const size_t ra = ((size_t)(2 * bp) * H + h0 + c) * P::L, rb = ra + (size_t)H * P::L;
-    process_pair<P, TIO, ACC16, HOLD, K1>(cur, S, spec(c), y + ra, y + rb, F0, F1, TW1, TW2, lane);
+    process_pair<P, TIO, ACC16, HOLD, K1, HERM>(cur, S, spec(c), y + ra, y + rb, F0, F1, TW1, TW2, lane);
   }
   for (int p = wave + NW; p < npairs; p += NW) {
     // compiler-only barrier: keeps the table reads inside the loop (hoisting them
@@ -524,7 +590,7 @@ __global__ void __launch_bounds__(64 * NW)
     const int c = p / BP, bp = p - c * BP;
     const size_t ra = ((size_t)(2 * bp) * H + h0 + c) * P::L, rb = ra + (size_t)H * P::L;
     issue_pair_loads<P, TIO>(u + ra, u + rb, cur, ln);
-    process_pair<P, TIO, ACC16, HOLD, K1>(cur, S, spec(c), y + ra, y + rb, F0, F1, TW1, TW2, ln);
+    process_pair<P, TIO, ACC16, HOLD, K1, HERM>(cur, S, spec(c), y + ra, y + rb, F0, F1, TW1, TW2, ln);
   }
 }
 

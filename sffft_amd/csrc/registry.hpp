@@ -16,10 +16,13 @@ typedef hipError_t (*launch_fn)(const void* u, const void* kf, void* y, int B, i
 //           of `waves` wavefronts takes `channels` channels and shares their spectra
 //           and the DFT and twiddle tables in LDS (fftconv_wave.hpp; two-stage
 //           plans, seqs = 2)
+//   launch_complex: the same plan for complex filters (whole, non-Hermitian spectra
+//           from sffft_spectrum_complex, fp32 accumulation); mode 1 only, else null
 struct Entry {
   int L, r0, r1, r2, waves, seqs, mode, channels, lds_bytes;
   launch_fn launch[2][2];
   const void* func[2][2];
+  launch_fn launch_complex[2][2];
 };
 
 // Defined by conv_inst.hip compiled once per length.

@@ -144,6 +144,12 @@ class _LongConvFn(torch.autograd.Function):
         return du, dk, None, None
 
 
+def _drop_cached(owner_ref, key) -> None:
+    owner = owner_ref()
+    if owner is not None:
+        owner._cache.pop(key, None)
+
+
 class LongConv:
     """Causal long convolution y = causal_conv(u, k) with the filter spectrum cached.
 
@@ -176,7 +182,9 @@ class LongConv:
             return hit[2]
         kf = torch.ops.sffft.spectrum(k.detach(), fields)
         if not same:
-            weakref.finalize(k, self._cache.pop, id(k), None)
+            # the finalizer holds the cache only through a weak reference to this object, so
+            # a long-lived filter does not keep a dropped LongConv's spectra alive
+            weakref.finalize(k, _drop_cached, weakref.ref(self), id(k))
         self._cache[id(k)] = (weakref.ref(k), key, kf)
         self.spectra_computed += 1
         return kf

@@ -48,9 +48,12 @@ def test_plan_validation():
     assert sf.plan_check(1024, P("64x32", 12, seqs=1, mode=1, channels=3)) == sf.SFFFT_EINVAL  # pairs only
     assert sf.plan_check(4096, P("32x16x16", 4, seqs=2, mode=1)) == sf.SFFFT_EINVAL  # two-stage only
     assert sf.plan_check(1024, P("64x32", 4, channels=2)) == sf.SFFFT_EINVAL  # channels: mode 1 only
-    # LDS of a wave plan: tables (DFT fragments, two twiddle tables) + one spectrum per channel
-    # + a 16-row operand scratch per wavefront
-    assert sf.lds_bytes(1024, P("64x32", 12, seqs=2, mode=1, channels=3)) == (32768 + 8192 + 32768 + 3 * 16384 +
+    # LDS of a wave plan: tables (DFT fragments, two twiddle tables) + one Hermitian half
+    # spectrum per channel (33 columns k0 = 0..32 of 2*8+1 float4, the three channels in whole
+    # 1 KB runs) + a 16-row operand scratch per wavefront
+    half = 33 * 17 * 16
+    assert sf.lds_bytes(1024, P("64x32", 12, seqs=2, mode=1, channels=3)) == (32768 + 8192 + 32768 +
+                                                                            (3 * half + 1023) // 1024 * 1024 +
                                                                             12 * 16 * 36 * 4)
     assert sf.lds_bytes(1024, P("64x16", 4)) == 0
 

@@ -4,9 +4,10 @@ oracle, through the C ABI.
 Every compiled plan (column radix 16, 32 or 64 with row plans 16x16, 32x32, 64x32 and
 64x64, L = 2048 .. 131072) runs both I/O types on seeded inputs and is compared over all
 outputs with the oracle's fp64 FFT convolution (direct convolution at L = 2048). Bounds
-are those of the fused kernel: 5e-4 for fp32 I/O (6e-4 is not needed: the pass-A input
-enters as an fp16 value plus its remainder) and 3e-3 for bf16 I/O, whose error includes
-the rounding of inputs and outputs.
+are those of the fused kernel: 5e-4 for fp32 I/O (the pass-A input enters as an fp16
+value plus its remainder) and 3e-3 for bf16 I/O, whose error includes the rounding of
+inputs and outputs. The circular convolution, an operation the reference does not have,
+has its own fp32 bound (see its test).
 
 At the plans' own small L the result must also agree with the single-pass kernel to
 the same bound, and the bench configurations run at full B=8, H=768 through the
@@ -68,7 +69,7 @@ def test_long_matches_single_pass(dev):
     ref = oracle.conv(u, k)
     a = _run(dev, u, k, sf.long_plan("64x16x16"), "fp32")
     b = _run(dev, u, k, sf.default_plan(L, "fp32", B), "fp32")
-    assert oracle.rel_l2(a, ref) <= 5e-4 and oracle.rel_l2(b, ref) <= 6e-4
+    assert oracle.rel_l2(a, ref) <= 5e-4 and oracle.rel_l2(b, ref) <= 5e-4
     assert oracle.rel_l2(a, b.astype(np.float64)) <= 1e-3
 
 
@@ -203,4 +204,4 @@ def test_complex_input_conv(dev, L, plan_of):
         ref = np.fft.ifft(np.fft.fft(x64, 2 * L) * np.fft.fft(k64, 2 * L)[None], axis=-1)[..., :L]
     err = np.linalg.norm(y - ref) / np.linalg.norm(ref)
     print(f"case complex L={L} {plan!r} rel_l2={err:.3e}", flush=True)
-    assert err <= 6e-4, (L, repr(plan), err)
+    assert err <= 5e-4, (L, repr(plan), err)

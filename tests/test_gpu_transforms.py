@@ -24,8 +24,9 @@ def crandn(rng, *shape):
 
 
 @pytest.mark.parametrize("batch,N", [(3, 2), (5, 4), (7, 16), (4, 64), (3, 128), (6, 1024), (2, 4096), (3, 8192),
-                                     (2, 65536), (1, 1 << 20)])
+                                     (2, 65536), (1, 1 << 20), (1, 1 << 22), (1, 1 << 24)])
 def test_fft_matches_numpy(batch, N):
+    """Up to N = 2^24, whose six radix-16 stages fill the stage table exactly."""
     print(f"fft batch={batch} N={N}", flush=True)
     x = crandn(np.random.default_rng(N + batch), batch, N)
     X = sf.fft(torch.from_numpy(x).to(DEV)).cpu().numpy()

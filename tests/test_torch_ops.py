@@ -6,6 +6,9 @@ the fp64 oracle against a brute-force anti-causal correlation.
 GPU: bit equality with the C-ABI path, torch.library.opcheck, the gradient against the oracle,
 the spectrum cache, torch.compile and graph capture.
 """
+import gc
+import weakref
+
 import numpy as np
 import pytest
 import torch
@@ -129,7 +132,7 @@ def test_input_gradient(dev, L):
     ref = oracle.conv(w_np[:, :, ::-1].copy(), k_np)[:, :, ::-1]
     err = oracle.rel_l2(u.grad.cpu().numpy(), ref)
     print(f"L={L} input-gradient rel_l2={err:.3e}", flush=True)
-    assert err <= 6e-4
+    assert err <= 5e-4
 
 
 @pytest.mark.gpu
@@ -151,7 +154,7 @@ def test_filter_gradient(dev, L, io):
     ref = r.reshape(B, H, L)[:, :, ::-1].sum(0)
     err = oracle.rel_l2(k.grad.cpu().numpy(), ref)
     print(f"L={L} {io} filter-gradient rel_l2={err:.3e}", flush=True)
-    assert err <= (6e-4 if io == "fp32" else 3e-3)
+    assert err <= (5e-4 if io == "fp32" else 3e-3)
     assert u.grad is not None and u.grad.dtype == u.dtype
 
 
@@ -195,6 +198,17 @@ def test_spectrum_cache(dev):
     k2 = k.clone()
     lc(u, k2)
     assert lc.spectra_computed == 3
+    # a freed filter drops its entry; a dropped LongConv releases its spectra even while
+    # the filters it has seen live on
+    del k2
+    gc.collect()
+    assert len(lc._cache) == 1
+    kf = weakref.ref(lc._cache[id(k)][2])
+    owner = weakref.ref(lc)
+    del lc
+    gc.collect()
+    assert owner() is None and kf() is None
+    assert k.is_cuda  # the filter itself is untouched
 
 
 @pytest.mark.gpu

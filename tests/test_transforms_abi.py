@@ -11,6 +11,10 @@ def test_work_bytes():
     assert lib.sffft_fft_work_bytes(4, 128) == 4 * 128 * 8
     assert lib.sffft_fft_work_bytes(4, 96) == 0  # not a power of two: rejected
     assert lib.sffft_fft_work_bytes(1, 1 << 25) == 0
+    # the largest length: six radix-16 stages (the stage table holds exactly six), so it is
+    # accepted and staged through a workspace of one sequence
+    assert lib.sffft_fft_work_bytes(1, 1 << 24) == (1 << 24) * 8
+    assert lib.sffft_fft_work_bytes(1, 1 << 21) == (1 << 21) * 8
     assert lib.sffft_fft_work_bytes(0, 64) == 0
     assert lib.sffft_fft2_work_bytes(2, 16, 8) == 0
     assert lib.sffft_fft2_work_bytes(2, 64, 128) == 2 * 64 * 128 * 8
@@ -31,6 +35,10 @@ def test_argument_errors_need_no_gpu():
     assert f(x, X, w, 1 << 40, 1 << 12, 1 << 20, 1, 1 << 20, 0, 1.0, null) == E  # batch * N > 2^31
     assert f(x, X, w, 1 << 20, 2, 128, 0, 128, 0, 1.0, null) == E              # stride 0
     assert f(x, X, w, 1 << 20, 2, 128, 1, 0, 0, 1.0, null) == E                # sequences alias
+    assert f(x, X, w, 1 << 20, 2, 128, 1, 1, 0, 1.0, null) == E                # overlapping sequences
+    assert f(x, X, w, 1 << 20, 4, 128, 2, 128, 0, 1.0, null) == E              # dist < N * stride, stride < batch
+    assert f(x, X, w, 1 << 20, 4, 128, 3, 1, 0, 1.0, null) == E                # interleaved, stride < batch * dist
+    assert f(x, ctypes.c_void_p((1 << 40) + 8), w, 1 << 20, 2, 128, 1, 128, 0, 1.0, null) == E  # x, X overlap
     assert f(x, X, w, 1 << 20, 2, 128, 1, 128, 2, 1.0, null) == E              # inverse not 0/1
     assert f(x, X, w, 2 * 128 * 8 - 8, 2, 128, 1, 128, 0, 1.0, null) == E      # workspace too small
     assert f(x, X, null, 1 << 20, 2, 128, 1, 128, 0, 1.0, null) == E           # workspace missing
