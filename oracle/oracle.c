@@ -17,7 +17,11 @@
  *                           pinned: equals the direct convolution to ~1e-14 for every plan.
  *   oracle_fourstep_fp16    same schedule with fp16 rounding of storage, operands, and
  *                           (optionally) the raw accumulator; pinned: fp64 mode of the same
- *                           code equals oracle_fourstep_conv; overflow rows equal +-inf.
+ *                           code equals oracle_fourstep_conv; mode 1 and mode 2 reproduce the
+ *                           published fp32- and fp16-accumulation errors per plan
+ *                           (results/gb10_allocator_sweep.csv) within 25%; mode 2 overflows to
+ *                           inf/nan at input scale 15000 where mode 1 stays within 1e-3, as
+ *                           tests/precision_smoke.sh:49-56 requires of the kernels.
  *   oracle_select_candidate src/selection.h:13-24         pinned: tests/selection_test.cpp
  *   oracle_relative_l2      src/selection.h:26-29         asserts + the reference header
  *                           compiled from the reference tree (oracle/_ref).

@@ -15,6 +15,8 @@ from typing import List, Optional, Tuple
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libsffft.so")
+# The race-check build (every wavefront-level LDS hand-off a real wait), for tests only.
+DEBUG_LIB_PATH = os.path.join(_HERE, "libsffft_debug.so")
 CLI_PATH = os.path.join(_HERE, "sffft")
 ROCFFT_LIB_PATH = os.path.join(_HERE, "libsffft_rocfft.so")
 HEADER_PATH = os.path.join(os.path.dirname(_HERE), "include", "sffft.h")
@@ -80,59 +82,64 @@ def lib() -> ctypes.CDLL:
     """Loads libsffft.so (built in-tree by `make -C sffft_amd`)."""
     global _lib
     if _lib is None:
-        if not os.path.exists(LIB_PATH):
-            raise RuntimeError(f"{LIB_PATH} is missing: build it with `make -C sffft_amd` "
-                               "(or __graft_entry__.build())")
-        # PyTorch ships its own HIP runtime under the same soname as /opt/rocm's.
-        # Import it first so libsffft.so binds to the runtime torch uses: two HIP
-        # runtimes in one process do not share devices, memory or streams.
-        try:
-            import torch  # noqa: F401
-        except ImportError:
-            pass
-        L = ctypes.CDLL(LIB_PATH)
-        P = ctypes.POINTER(Plan)
-        vp, ci, sz = ctypes.c_void_p, ctypes.c_int, ctypes.c_size_t
-        sigs = {
-            "sffft_plan_check": (ci, [ci, P]),
-            "sffft_plan_lds_bytes": (sz, [ci, P]),
-            "sffft_plan_occupancy": (ci, [ci, P, ctypes.POINTER(ci)]),
-            "sffft_plan_count": (ci, [ci]),
-            "sffft_plan_get": (ci, [ci, ci, P, ctypes.c_char_p, sz]),
-            "sffft_spectrum_bytes": (sz, [ci, ci]),
-            "sffft_spectrum": (ci, [vp, ci, ci, P, vp, vp, vp]),
-            "sffft_spectrum_from_natural": (ci, [vp, ci, ci, P, vp, vp]),
-            "sffft_conv_f32": (ci, [vp, vp, vp, ci, ci, ci, P, vp]),
-            "sffft_conv_bf16": (ci, [vp, vp, vp, ci, ci, ci, P, vp]),
-            "sffft_conv_complex_f32": (ci, [vp, vp, vp, ci, ci, ci, P, vp]),
-            "sffft_conv_complex_bf16": (ci, [vp, vp, vp, ci, ci, ci, P, vp]),
-            "sffft_work_bytes": (sz, [ci, ci, ci, P]),
-            "sffft_conv_long_f32": (ci, [vp, vp, vp, vp, sz, ci, ci, ci, P, vp]),
-            "sffft_conv_long_bf16": (ci, [vp, vp, vp, vp, sz, ci, ci, ci, P, vp]),
-            "sffft_spectrum_circular": (ci, [vp, ci, ci, P, vp, vp, vp]),
-            "sffft_spectrum_complex": (ci, [vp, vp, ci, ci, P, vp, vp, vp]),
-            "sffft_circconv_long_f32": (ci, [vp, vp, vp, vp, sz, ci, ci, ci, P, vp]),
-            "sffft_circconv_long_bf16": (ci, [vp, vp, vp, vp, sz, ci, ci, ci, P, vp]),
-            "sffft_fft_work_bytes": (sz, [ci, ci]),
-            "sffft_fft_c2c": (ci, [vp, vp, vp, sz, ci, ci, ctypes.c_longlong, ctypes.c_longlong, ci,
-                                   ctypes.c_float, vp]),
-            "sffft_fft2_work_bytes": (sz, [ci, ci, ci]),
-            "sffft_fft2_c2c": (ci, [vp, vp, vp, sz, ci, ci, ci, ci, ctypes.c_float, vp]),
-            "sffft_circconv2d_work_bytes": (sz, [ci, ci, ci, ci]),
-            "sffft_circconv2d_f32": (ci, [vp, vp, vp, vp, sz, ci, ci, ci, ci, vp]),
-            "sffft_to_bf16": (ci, [vp, vp, sz, vp]),
-            "sffft_dispatch_floor": (ci, [ci, ci, ci, P, vp]),
-            "sffft_dft_table": (ci, [vp, sz]),
-            "sffft_select_candidate": (ci, [ctypes.POINTER(Candidate), ci, ctypes.c_double, ctypes.c_char_p]),
-            "sffft_relative_l2": (ctypes.c_double, [ctypes.c_double, ctypes.c_double]),
-            "sffft_strerror": (ctypes.c_char_p, [ci]),
-            "sffft_last_error": (ctypes.c_char_p, []),
-        }
-        for name, (res, args) in sigs.items():
-            f = getattr(L, name)
-            f.restype, f.argtypes = res, args
-        _lib = L
+        _lib = load_library(LIB_PATH)
     return _lib
+
+
+def load_library(path: str) -> ctypes.CDLL:
+    """Loads a build of the C ABI from `path` with the argument types of include/sffft.h."""
+    if not os.path.exists(path):
+        raise RuntimeError(f"{path} is missing: build it with `make -C sffft_amd` "
+                           "(or __graft_entry__.build())")
+    # PyTorch ships its own HIP runtime under the same soname as /opt/rocm's.
+    # Import it first so the library binds to the runtime torch uses: two HIP
+    # runtimes in one process do not share devices, memory or streams.
+    try:
+        import torch  # noqa: F401
+    except ImportError:
+        pass
+    L = ctypes.CDLL(path)
+    P = ctypes.POINTER(Plan)
+    vp, ci, sz = ctypes.c_void_p, ctypes.c_int, ctypes.c_size_t
+    sigs = {
+        "sffft_plan_check": (ci, [ci, P]),
+        "sffft_plan_lds_bytes": (sz, [ci, P]),
+        "sffft_plan_occupancy": (ci, [ci, P, ctypes.POINTER(ci)]),
+        "sffft_plan_count": (ci, [ci]),
+        "sffft_plan_get": (ci, [ci, ci, P, ctypes.c_char_p, sz]),
+        "sffft_spectrum_bytes": (sz, [ci, ci]),
+        "sffft_spectrum": (ci, [vp, ci, ci, P, vp, vp, vp]),
+        "sffft_spectrum_from_natural": (ci, [vp, ci, ci, P, vp, vp]),
+        "sffft_conv_f32": (ci, [vp, vp, vp, ci, ci, ci, P, vp]),
+        "sffft_conv_bf16": (ci, [vp, vp, vp, ci, ci, ci, P, vp]),
+        "sffft_conv_complex_f32": (ci, [vp, vp, vp, ci, ci, ci, P, vp]),
+        "sffft_conv_complex_bf16": (ci, [vp, vp, vp, ci, ci, ci, P, vp]),
+        "sffft_work_bytes": (sz, [ci, ci, ci, P]),
+        "sffft_conv_long_f32": (ci, [vp, vp, vp, vp, sz, ci, ci, ci, P, vp]),
+        "sffft_conv_long_bf16": (ci, [vp, vp, vp, vp, sz, ci, ci, ci, P, vp]),
+        "sffft_spectrum_circular": (ci, [vp, ci, ci, P, vp, vp, vp]),
+        "sffft_spectrum_complex": (ci, [vp, vp, ci, ci, P, vp, vp, vp]),
+        "sffft_circconv_long_f32": (ci, [vp, vp, vp, vp, sz, ci, ci, ci, P, vp]),
+        "sffft_circconv_long_bf16": (ci, [vp, vp, vp, vp, sz, ci, ci, ci, P, vp]),
+        "sffft_fft_work_bytes": (sz, [ci, ci]),
+        "sffft_fft_c2c": (ci, [vp, vp, vp, sz, ci, ci, ctypes.c_longlong, ctypes.c_longlong, ci,
+                               ctypes.c_float, vp]),
+        "sffft_fft2_work_bytes": (sz, [ci, ci, ci]),
+        "sffft_fft2_c2c": (ci, [vp, vp, vp, sz, ci, ci, ci, ci, ctypes.c_float, vp]),
+        "sffft_circconv2d_work_bytes": (sz, [ci, ci, ci, ci]),
+        "sffft_circconv2d_f32": (ci, [vp, vp, vp, vp, sz, ci, ci, ci, ci, vp]),
+        "sffft_to_bf16": (ci, [vp, vp, sz, vp]),
+        "sffft_dispatch_floor": (ci, [ci, ci, ci, P, vp]),
+        "sffft_dft_table": (ci, [vp, sz]),
+        "sffft_select_candidate": (ci, [ctypes.POINTER(Candidate), ci, ctypes.c_double, ctypes.c_char_p]),
+        "sffft_relative_l2": (ctypes.c_double, [ctypes.c_double, ctypes.c_double]),
+        "sffft_strerror": (ctypes.c_char_p, [ci]),
+        "sffft_last_error": (ctypes.c_char_p, []),
+    }
+    for name, (res, args) in sigs.items():
+        f = getattr(L, name)
+        f.restype, f.argtypes = res, args
+    return L
 
 
 def strerror(code: int) -> str:

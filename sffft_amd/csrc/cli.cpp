@@ -171,6 +171,17 @@ double nrand() {
   return std::sqrt(-2 * std::log(u1)) * std::cos(2 * M_PI * u2);
 }
 
+// The calibration inputs of one length, drawn from the running generator state:
+// u [BH][L] ~ N(0,1) * input_scale in (b, h, n) order, then k [H][L] with the decay
+// a = 1 / (4 + L h / H) (src/sffft.cu:339-341).
+void generate_inputs(size_t BH, int H, int L, double input_scale, float* u, float* k) {
+  for (size_t i = 0; i < BH * L; i++) u[i] = (float)(nrand() * input_scale);
+  for (int h = 0; h < H; h++) {
+    const double a = 1.0 / (4.0 + (double)L * h / H);
+    for (int n = 0; n < L; n++) k[(size_t)h * L + n] = (float)(nrand() * std::exp(-a * n) * std::sqrt(2 * a));
+  }
+}
+
 uint16_t bf16_bits(float f) {  // round to nearest even (the device conversion's rule)
   uint32_t x;
   std::memcpy(&x, &f, 4);
@@ -240,11 +251,7 @@ struct Bench {
     }
     float* hkv = mem.host_view(dk);
     hk.resize((size_t)H * L);
-    for (size_t i = 0; i < BH * L; i++) hu[i] = (float)(nrand() * input_scale);
-    for (int h = 0; h < H; h++) {
-      const double a = 1.0 / (4.0 + (double)L * h / H);
-      for (int n = 0; n < L; n++) hk[(size_t)h * L + n] = (float)(nrand() * std::exp(-a * n) * std::sqrt(2 * a));
-    }
+    generate_inputs(BH, H, L, input_scale, hu, hk.data());
     if (hkv) std::memcpy(hkv, hk.data(), hk.size() * 4);
     mem.upload(du, hu, BH * L);
     if (!hkv) mem.upload(dk, hk.data(), hk.size());
@@ -397,10 +404,13 @@ struct Bench {
 void usage() {
   printf(
       "Usage: sffft [B H [L]] [--max-error REL_L2] [--io fp32|bf16|any] [--seed N] [--input-scale SCALE] "
-      "[--allocator device|managed|mapped|hybrid] [--kernel legacy|cached|auto] [--memory-info]\n"
+      "[--allocator device|managed|mapped|hybrid] [--kernel legacy|cached|auto] [--memory-info] "
+      "[--dump-inputs FILE]\n"
       "L: 0 (all of 128..8192) or a power of two from 128 to 16384. Defaults: B=8 H=768, io=fp32.\n"
       "--max-error selects the fastest passing fused plan on these calibration inputs.\n"
-      "Error is measured against the rocFFT fp32 pipeline; no match exits 2. Invalid arguments exit 1.\n");
+      "Error is measured against the rocFFT fp32 pipeline; no match exits 2. Invalid arguments exit 1.\n"
+      "--dump-inputs writes the calibration inputs of length L (u [B][H][L] then k [H][L], raw fp32)\n"
+      "to FILE and exits without touching the GPU (needs L).\n");
 }
 
 }  // namespace
@@ -411,6 +421,7 @@ int main(int argc, char** argv) {
   const char* io = "fp32";
   Alloc allocation = Alloc::Device;
   bool memory_info = false;
+  const char* dump_path = nullptr;
   int kernel_mode = 0;  // 0 legacy, 1 cached, 2 auto
   for (int i = 1; i < argc; i++) {
     const char* arg = argv[i];
@@ -422,6 +433,14 @@ int main(int argc, char** argv) {
     }
     if (!strcmp(arg, "--memory-info")) {
       memory_info = true;
+      continue;
+    }
+    if (!strcmp(arg, "--dump-inputs")) {
+      if (++i == argc) {
+        usage();
+        return 1;
+      }
+      dump_path = argv[i];
       continue;
     }
     if (!strcmp(arg, "--allocator")) {
@@ -518,6 +537,22 @@ int main(int argc, char** argv) {
     fprintf(stderr,
             "B and H must be positive with B*H <= INT_MAX; L must be 0 or 128,256,512,1024,2048,4096,8192,16384\n");
     return 1;
+  }
+  if (dump_path) {  // host only: the inputs the run of length `only` would use
+    if (!only) {
+      fprintf(stderr, "--dump-inputs needs L\n");
+      return 1;
+    }
+    const size_t BH = (size_t)B * H;
+    std::vector<float> hu(BH * only), hk((size_t)H * only);
+    generate_inputs(BH, H, only, input_scale, hu.data(), hk.data());
+    FILE* f = fopen(dump_path, "wb");
+    if (!f || fwrite(hu.data(), 4, hu.size(), f) != hu.size() || fwrite(hk.data(), 4, hk.size(), f) != hk.size() ||
+        fclose(f)) {
+      fprintf(stderr, "--dump-inputs: cannot write %s\n", dump_path);
+      return 1;
+    }
+    return 0;
   }
   hipDeviceProp_t p;
   HK(hipGetDeviceProperties(&p, 0));

@@ -237,6 +237,29 @@ __device__ __forceinline__ void twiddle4(int a, int b0, float sc, float* wr, flo
 }
 
 // 8-half operand: slots 0..3 from the real plane, 4..7 from the imaginary plane.
+// Orders one wavefront's LDS accesses across its lanes (a lane reads what other lanes
+// of the same wavefront wrote, or overwrites what they read). A wavefront's LDS
+// operations complete in issue order, so the product build needs only a compiler
+// barrier: the compiler models each lane alone and would otherwise reuse a lane's
+// earlier reads or move writes above reads. The SFFFT_DEBUG_BARRIERS build also waits
+// until every LDS operation of the wavefront has completed, so it cannot depend on the
+// in-order completion; its outputs are compared bit for bit with the product build's.
+__device__ __forceinline__ void wave_lds_fence() {
+#ifdef SFFFT_DEBUG_BARRIERS
+  __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
+  __builtin_amdgcn_wave_barrier();
+#endif
+  __asm__ volatile("" ::: "memory");
+}
+
+// The same wait in the SFFFT_DEBUG_BARRIERS build only, where the product build relies
+// on program order alone (a wavefront overwriting LDS its lanes have read).
+__device__ __forceinline__ void debug_lds_fence() {
+#ifdef SFFFT_DEBUG_BARRIERS
+  wave_lds_fence();
+#endif
+}
+
 __device__ __forceinline__ h8 lds_frag(const _Float16* re, const _Float16* im, int pos) {
   const h4 a = *reinterpret_cast<const h4*>(re + pos);
   const h4 b = *reinterpret_cast<const h4*>(im + pos);
@@ -739,6 +762,7 @@ __device__ __forceinline__ void phase2_s3(_Float16* re, _Float16* im, const floa
       }
     }
     // inverse over k1 and the last twiddle
+    debug_lds_fence();  // the row's reads (stage over n1) before its write-back below
 #pragma unroll
     for (int nt = 0; nt < T2; nt++) {
 #pragma unroll

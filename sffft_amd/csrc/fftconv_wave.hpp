@@ -312,12 +312,10 @@ __device__ __forceinline__ void pair_operands(const PairLoads<P, TIO>& d, TIO* S
           *reinterpret_cast<u32x4*>(S + (e / M) * PITCH + e % M) = d.c[i];
         }
       }
-      // A lane reads what other lanes wrote. The wavefront's LDS operations complete
-      // in order, so no instruction is needed, but the compiler models each lane
-      // alone: without these compiler-only barriers a lane that wrote nothing here
-      // would reuse its reads of the previous block, and writes could be moved above
-      // the previous block's reads.
-      __asm__ volatile("" ::: "memory");
+      // A lane reads what other lanes wrote: without the fences a lane that wrote
+      // nothing here would reuse its reads of the previous block, and writes could be
+      // moved above the previous block's reads.
+      wave_lds_fence();
 #pragma unroll
       for (int mt = 0; mt < P::MT; mt++)
 #pragma unroll
@@ -326,7 +324,7 @@ __device__ __forceinline__ void pair_operands(const PairLoads<P, TIO>& d, TIO* S
           const float v = live ? io_to_f32_lds(S + (4 * g + j) * PITCH + 16 * mt + r) : 0.f;
           a[mt][ks][4 * sq + j] = (_Float16)v;
         }
-      __asm__ volatile("" ::: "memory");
+      wave_lds_fence();
     }
 }
 
@@ -349,8 +347,8 @@ __device__ __forceinline__ void store_rows(TIO* S, const f4 (&z)[P::MT], TIO* __
   const int c = lane & 15, g = lane >> 4;
 #pragma unroll
   for (int t = 0; t < P::MT; t++) put4(S + c * PITCH + 16 * t + 4 * g, z[t]);
-  // other lanes' writes are read below (see pair_operands)
-  __asm__ volatile("" ::: "memory");
+  // other lanes' writes are read below
+  wave_lds_fence();
 #pragma unroll
   for (int i = 0; i < ROUNDS; i++) {
     const int q = i * 64 + lane, row = q / CPR, col = (q % CPR) * EPC;
@@ -358,7 +356,7 @@ __device__ __forceinline__ void store_rows(TIO* S, const f4 (&z)[P::MT], TIO* __
       __builtin_nontemporal_store(*reinterpret_cast<const u32x4*>(S + row * PITCH + col),
                                   reinterpret_cast<u32x4*>(y + row * M + col));
   }
-  __asm__ volatile("" ::: "memory");
+  wave_lds_fence();
 }
 
 // Every stage of one pair, from its loaded operands to the stored outputs; SP is the
@@ -560,7 +558,11 @@ __global__ void __launch_bounds__(64 * NW)
   __asm__ volatile("" ::: "memory");
   if (early) {
     issue_first();
+#ifdef SFFFT_DEBUG_BARRIERS
+    wait_vmcnt<0>();  // the pair's loads too: the barrier below then needs no count
+#else
     wait_vmcnt<pair_load_issues<P, TIO>()>();
+#endif
   } else {
     wait_vmcnt<0>();
   }

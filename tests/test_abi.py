@@ -13,10 +13,11 @@ def declared_functions():
     return sorted(set(re.findall(r"^\s*(?:const\s+)?[a-z_0-9]+\s*\*?\s*(sffft_[a-z0-9_]+)\s*\(", text, re.M)))
 
 
-def test_every_declared_symbol_is_exported():
+@pytest.mark.parametrize("path", [sf.LIB_PATH, sf.DEBUG_LIB_PATH], ids=["product", "debug-barriers"])
+def test_every_declared_symbol_is_exported(path):
     names = declared_functions()
     assert len(names) >= 16
-    lib = ctypes.CDLL(sf.LIB_PATH)
+    lib = ctypes.CDLL(path)
     for n in names:
         assert hasattr(lib, n), n
 

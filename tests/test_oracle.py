@@ -118,6 +118,50 @@ def test_fp16_model_reproduces_published_error_scale(radices):
     assert abs(err / PUBLISHED_FP32IO[radices] - 1) < 0.25, err
 
 
+# Published errors of the reference's fp16-accumulation kernels, fp32 I/O, same inputs
+# (results/gb10_allocator_sweep.csv:451,471,499,535,571,651).
+PUBLISHED_FP16ACC_FP32IO = {(16, 16, 1): 5.244e-4, (32, 16, 1): 5.324e-4, (32, 32, 1): 5.420e-4,
+                            (64, 32, 1): 6.085e-4, (16, 16, 16): 6.275e-4, (32, 32, 16): 6.199e-4}
+
+
+@pytest.mark.parametrize("radices", sorted(PUBLISHED_FP16ACC_FP32IO), ids=lambda r: "x".join(map(str, r)))
+def test_fp16_accumulation_model_reproduces_published_error_scale(radices):
+    """Mode 2 of the fp16 model (every raw accumulator rounded to fp16) lands within 25% of the
+    published fp16-accumulation error, and above the fp32-accumulation model (mode 1) on the
+    same inputs: the extra rounding is visible, so a mode 2 that silently behaved like mode 1
+    fails here."""
+    r0, r1, r2 = radices
+    L = r0 * r1 * r2 // 2
+    H = 768
+    u, k = oracle.ref_inputs(1, H, L)
+    y1, y2, refs = [], [], []
+    for h in range(0, H, H // 24):
+        kf = oracle.spectrum_p_order(k[h], r0, r1, r2)
+        y1.append(oracle.fourstep_conv(u[0, h], kf, r0, r1, r2, mode=1))
+        y2.append(oracle.fourstep_conv(u[0, h], kf, r0, r1, r2, mode=2))
+        refs.append(oracle.conv(u[:, h:h + 1], k[h:h + 1])[0, 0])
+    e1 = oracle.rel_l2(np.array(y1), np.array(refs))
+    e2 = oracle.rel_l2(np.array(y2), np.array(refs))
+    assert abs(e2 / PUBLISHED_FP16ACC_FP32IO[radices] - 1) < 0.25, e2
+    assert e2 > 1.2 * e1, (e1, e2)
+
+
+def test_fp16_accumulation_model_overflows_where_the_reference_does():
+    """tests/precision_smoke.sh:49-56 at B=1, H=1, L=128 (16x16): with input scale 15000 the
+    fp32-accumulation kernel stays within 1e-3 while fp16 accumulators overflow to inf/nan;
+    at 25000 the input itself leaves the fp16 range and every mode fails."""
+    u, k = oracle.ref_inputs(1, 1, 128, input_scale=15000.0)
+    kf = oracle.spectrum_p_order(k[0], 16, 16)
+    ref = oracle.conv(u, k)[0, 0]
+    y1 = oracle.fourstep_conv(u[0, 0], kf, 16, 16, mode=1)
+    assert np.isfinite(y1).all() and oracle.rel_l2(y1, ref) < 1e-3
+    assert not np.isfinite(oracle.fourstep_conv(u[0, 0], kf, 16, 16, mode=2)).all()
+    u, k = oracle.ref_inputs(1, 1, 128, input_scale=25000.0)
+    kf = oracle.spectrum_p_order(k[0], 16, 16)
+    for mode in (1, 2):
+        assert not np.isfinite(oracle.fourstep_conv(u[0, 0], kf, 16, 16, mode=mode)).all()
+
+
 def test_fp16_rounding_matches_numpy_and_overflows():
     rng = np.random.default_rng(0)
     xs = np.concatenate([rng.standard_normal(2000) * 10.0 ** rng.integers(-8, 5, 2000),
