@@ -29,6 +29,7 @@ extern "C" {
 #define SFFFT_ENOPLAN 2     /* the plan is valid but was not compiled into this library */
 #define SFFFT_EHIP 3        /* the HIP runtime reported an error */
 #define SFFFT_ENOTFOUND 4   /* no candidate/plan matches the request */
+#define SFFFT_ESCRATCH 5    /* more workspace than sffft_spectrum_noalloc's static scratch */
 
 /* A transform plan: N = 2L = r0*r1*r2 (r2 = 1 for two-stage plans), radices in
  * {16,32,64}. Mirrors Plan<R0,R1,R2> and the W template argument of fftconv
@@ -93,6 +94,16 @@ size_t sffft_spectrum_bytes(int H, int L);
  * Replaces: zero-pad + cufftExecC2C(FORWARD) + permuteK (src/sffft.cu:342-344,365,384,283-288).
  * Arithmetic: fp64 accumulation and twiddles, fp32 storage between the stages. */
 int sffft_spectrum(const float* k, int H, int L, const sffft_plan* plan, void* kf, void* work, void* stream);
+
+/* sffft_spectrum without the `work` argument, for callers that cannot allocate (code under
+ * HIP graph capture, serving loops, harnesses that forbid hipMalloc). No counterpart in the
+ * reference. It stages the channels through a static device array of 32 MiB per GPU (held
+ * until the process ends; 2L*8 bytes per channel, so the channels run in chunks) and calls
+ * no hipMalloc, hipFree or allocating routine; its output is bit-identical to
+ * sffft_spectrum's. Every call on one GPU shares that GPU's array: calls that overlap on one
+ * GPU (two streams, two host threads) race. SFFFT_ESCRATCH if one channel needs more than
+ * the array (never for a valid L). */
+int sffft_spectrum_noalloc(const float* k, int H, int L, const sffft_plan* plan, void* kf, void* stream);
 
 /* Complex input: the spectrum of the complex filter kr + i*ki (kr, ki [H][L] fp32) for a plan
  * with two sequences per transform (seqs = 2; every mode-1 and mode-2 plan). With it,

@@ -21,7 +21,7 @@ CLI_PATH = os.path.join(_HERE, "sffft")
 ROCFFT_LIB_PATH = os.path.join(_HERE, "libsffft_rocfft.so")
 HEADER_PATH = os.path.join(os.path.dirname(_HERE), "include", "sffft.h")
 
-SFFFT_OK, SFFFT_EINVAL, SFFFT_ENOPLAN, SFFFT_EHIP, SFFFT_ENOTFOUND = 0, 1, 2, 3, 4
+SFFFT_OK, SFFFT_EINVAL, SFFFT_ENOPLAN, SFFFT_EHIP, SFFFT_ENOTFOUND, SFFFT_ESCRATCH = 0, 1, 2, 3, 4, 5
 LENGTHS = (128, 256, 512, 1024, 2048, 4096, 8192, 16384)
 # multi-pass plans (mode 2) beyond one CU's LDS
 LONG_LENGTHS = (32768, 65536, 131072)
@@ -110,6 +110,7 @@ def load_library(path: str) -> ctypes.CDLL:
         "sffft_spectrum_bytes": (sz, [ci, ci]),
         "sffft_spectrum": (ci, [vp, ci, ci, P, vp, vp, vp]),
         "sffft_spectrum_from_natural": (ci, [vp, ci, ci, P, vp, vp]),
+        "sffft_spectrum_noalloc": (ci, [vp, ci, ci, P, vp, vp]),
         "sffft_conv_f32": (ci, [vp, vp, vp, ci, ci, ci, P, vp]),
         "sffft_conv_bf16": (ci, [vp, vp, vp, ci, ci, ci, P, vp]),
         "sffft_conv_complex_f32": (ci, [vp, vp, vp, ci, ci, ci, P, vp]),

@@ -2,6 +2,7 @@
 // preparation, the fused convolution launch and the host-side selector.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <climits>
 #include <cmath>
 #include <cstring>
@@ -16,6 +17,13 @@
 #include "longconv.hpp"
 #include "registry.hpp"
 #include "transforms.hpp"
+
+// Workspace of sffft_spectrum_noalloc, the one entry point that allocates nothing: a
+// static device array, one per GPU the library runs on, held until the process ends.
+// Host code never uses its name as an address (that is a host-side stand-in): the device
+// address comes from hipGetSymbolAddress, once per device (scratch_for_device).
+static constexpr size_t SFFFT_SCRATCH_BYTES = (size_t)32 << 20;
+static __device__ __align__(256) unsigned char scratch[SFFFT_SCRATCH_BYTES];
 
 namespace sffft {
 namespace {
@@ -224,6 +232,26 @@ void build_twiddles(int r0, int r1, std::vector<float>& t) {
         }
 }
 
+std::mutex g_scratch_mu;
+void* g_scratch[256];  // per device: the device address of `scratch`
+
+// The current device's copy of `scratch`, looked up on the first call on that device.
+int scratch_for_device(void** out) {
+  int dev = 0;
+  hipError_t err = hipGetDevice(&dev);
+  if (err != hipSuccess) return hip_status(err, "hipGetDevice");
+  if (dev < 0 || dev >= 256) return SFFFT_EINVAL;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch[dev]) {
+    void* p = nullptr;
+    if ((err = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch))) != hipSuccess)
+      return hip_status(err, "hipGetSymbolAddress(scratch)");
+    g_scratch[dev] = p;
+  }
+  *out = g_scratch[dev];
+  return SFFFT_OK;
+}
+
 std::mutex g_tw_mu;
 std::map<std::pair<int, int>, void*> g_tw[256];  // per device: (r0, r1) -> table
 
@@ -367,22 +395,19 @@ __global__ void spectrum_permute_kernel(const float2* __restrict__ src, float2* 
 // (WavePlan::hs_index): per channel, (r0/2 + 1) columns k0 of PITCH = 8*(r1/16) + 1
 // float4; float4 (k0*PITCH + (kt*2 + q)*4 + g) holds k1 = 16kt + 4g + 2q and +1, i.e.
 // K[k0 + r0*k1]. Column r0/2 holds conj(K[r0/2 + r0*(r1 - 1 - k1)]) at k1; the last float4
-// of each column is zero padding. src as in spectrum_permute_kernel; channels are
-// consecutive (2*(r0/2 + 1)*PITCH complex values each), and the rest of the H*N buffer
-// is zeroed, so the whole buffer is a function of the filter.
-__global__ void spectrum_half_kernel(const float2* __restrict__ src, float2* __restrict__ kf, int H, int r0, int r1,
-                                     int natural, float scale) {
+// of each column is zero padding. src as in spectrum_permute_kernel, for the H channels
+// from channel h0 on; channels are consecutive in kf (C = 2*(r0/2 + 1)*PITCH complex
+// values each).
+__global__ void spectrum_half_kernel(const float2* __restrict__ src, float2* __restrict__ kf, int H, int h0, int r0,
+                                     int r1, int natural, float scale) {
   const int pitch = 8 * (r1 / 16) + 1, C = 2 * (r0 / 2 + 1) * pitch, N = r0 * r1;
   const size_t gid = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (gid >= (size_t)H * N) return;
-  if (gid >= (size_t)H * C) {
-    kf[gid] = make_float2(0.f, 0.f);
-    return;
-  }
+  if (gid >= (size_t)H * C) return;
+  float2* out = kf + (size_t)h0 * C + gid;
   const int h = (int)(gid / C), i = (int)(gid % C);
   const int f = i >> 1, e = i & 1, k0 = f / pitch, rem = f % pitch;
   if (rem == pitch - 1) {
-    kf[gid] = make_float2(0.f, 0.f);
+    *out = make_float2(0.f, 0.f);
     return;
   }
   const int g = rem & 3, q = (rem >> 2) & 1, kt = rem >> 3;
@@ -391,7 +416,14 @@ __global__ void spectrum_half_kernel(const float2* __restrict__ src, float2* __r
   const int kk1 = mid ? r1 - 1 - k1 : k1;
   const int sidx = natural ? k0 + r0 * kk1 : k0 * r1 + kk1;
   const float2 v = src[(size_t)h * N + sidx];
-  kf[gid] = make_float2(v.x * scale, (mid ? -v.y : v.y) * scale);
+  *out = make_float2(v.x * scale, (mid ? -v.y : v.y) * scale);
+}
+
+// Zeroes n complex values (the part of a spectrum buffer a Hermitian half leaves unused,
+// so the whole buffer is a function of the filter); a kernel, so it can be captured.
+__global__ void zero_fill_kernel(float2* __restrict__ p, size_t n) {
+  const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = make_float2(0.f, 0.f);
 }
 
 __global__ void to_bf16_kernel(const float* __restrict__ x, uint16_t* __restrict__ y, size_t n) {
@@ -498,40 +530,53 @@ int long_plans_for(int L, const LongEntry** out, int cap) {
 }
 
 // imag: k is the imaginary part of a complex filter; its spectrum is added times i to kf
-// Launches the gather of a p-order (natural = 0) or natural-order spectrum into the
-// kernel order of the plan: the Hermitian half for wave plans (mode 1) unless `whole`
-// (complex filters), else the whole spectrum.
+// Launches the gather of a p-order (natural = 0) or natural-order spectrum src of the H
+// channels from channel h0 on into the kernel order of the plan: the Hermitian half for
+// wave plans (mode 1) unless `whole` (complex filters), else the whole spectrum. kf is
+// the spectrum of all Htot channels; the gather of the last channels also zeroes what a
+// Hermitian half leaves unused.
 int permute_launch(const float2* src, float2* kf, int H, const sffft_plan* plan, int natural, int imag, int whole,
-                   hipStream_t s) {
+                   hipStream_t s, int h0 = 0, int Htot = -1) {
+  if (Htot < 0) Htot = H;
+  const size_t N = (size_t)plan->r0 * plan->r1 * plan->r2;
   if (plan->mode == 1 && !whole) {
-    const size_t total = (size_t)H * plan->r0 * plan->r1;
-    hipLaunchKernelGGL(spectrum_half_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, src, kf, H,
+    const size_t C = (size_t)2 * (plan->r0 / 2 + 1) * (8 * (plan->r1 / 16) + 1), total = (size_t)H * C;
+    hipLaunchKernelGGL(spectrum_half_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, src, kf, H, h0,
                        plan->r0, plan->r1, natural, last_stage_scale(plan));
+    if (h0 + H == Htot) {
+      const size_t tail = (size_t)Htot * (N - C);
+      hipLaunchKernelGGL(zero_fill_kernel, dim3((unsigned)((tail + 255) / 256)), dim3(256), 0, s,
+                         kf + (size_t)Htot * C, tail);
+    }
   } else {
-    const size_t total = (size_t)H * plan->r0 * plan->r1 * plan->r2;
-    hipLaunchKernelGGL(spectrum_permute_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, src, kf, H,
-                       plan->r0, plan->r1, plan->r2, plan->mode, natural, last_stage_scale(plan), imag);
+    const size_t total = (size_t)H * N;
+    hipLaunchKernelGGL(spectrum_permute_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, src,
+                       kf + (size_t)h0 * N, H, plan->r0, plan->r1, plan->r2, plan->mode, natural,
+                       last_stage_scale(plan), imag);
   }
   return hip_status(hipGetLastError(), "spectrum permute launch");
 }
 
+// Spectrum of the H filter rows from channel h0 on (all Htot of them when Htot < 0),
+// staged through `work` (H * N complex64).
 int spectrum_impl(const float* k, int H, int L, int klen, const sffft_plan* plan, void* kf, void* work,
-                  void* stream, int imag = 0, int whole = 0) {
+                  void* stream, int imag = 0, int whole = 0, int h0 = 0, int Htot = -1) {
   if (!k || !kf || !work || H < 1 || kf == work) return SFFFT_EINVAL;
   const int rc = check_shape(L, plan);
   if (rc) return rc;
   const int N = 2 * L, S = plan->r2 > 1 ? 3 : 2;
   hipStream_t s = (hipStream_t)stream;
   float2* w = static_cast<float2*>(work);
+  const float* kh = k + (size_t)h0 * klen;
   for (int J = 0; J < S; J++) {
     const int R = J == 0 ? plan->r0 : J == 1 ? plan->r1 : plan->r2;
     const size_t threads = (size_t)H * (N / R);
-    hipLaunchKernelGGL(spectrum_stage_kernel, dim3((unsigned)((threads + 127) / 128)), dim3(128), 0, s, k, w, H,
+    hipLaunchKernelGGL(spectrum_stage_kernel, dim3((unsigned)((threads + 127) / 128)), dim3(128), 0, s, kh, w, H,
                        klen, plan->r0, plan->r1, plan->r2, J);
     const int st = hip_status(hipGetLastError(), "spectrum stage launch");
     if (st) return st;
   }
-  return permute_launch(w, static_cast<float2*>(kf), H, plan, 0, imag, whole, s);
+  return permute_launch(w, static_cast<float2*>(kf), H, plan, 0, imag, whole, s, h0, Htot);
 }
 }  // namespace
 }  // namespace sffft
@@ -613,6 +658,24 @@ size_t sffft_spectrum_bytes(int H, int L) {
 
 int sffft_spectrum(const float* k, int H, int L, const sffft_plan* plan, void* kf, void* work, void* stream) {
   return spectrum_impl(k, H, L, L, plan, kf, work, stream);
+}
+
+int sffft_spectrum_noalloc(const float* k, int H, int L, const sffft_plan* plan, void* kf, void* stream) {
+  if (!k || !kf || H < 1) return SFFFT_EINVAL;
+  int rc = check_shape(L, plan);
+  if (rc) return rc;
+  const size_t per = (size_t)2 * L * 8;  // one channel staged through the workspace
+  if (per > SFFFT_SCRATCH_BYTES) {
+    snprintf(g_last_error, sizeof(g_last_error), "sffft_spectrum_noalloc: one channel needs %zu bytes of "
+             "workspace, the static scratch holds %zu", per, SFFFT_SCRATCH_BYTES);
+    return SFFFT_ESCRATCH;
+  }
+  void* work = nullptr;
+  if ((rc = scratch_for_device(&work))) return rc;
+  const int chunk = (int)std::min<size_t>((size_t)H, SFFFT_SCRATCH_BYTES / per);
+  for (int h0 = 0; h0 < H; h0 += chunk)
+    if ((rc = spectrum_impl(k, std::min(chunk, H - h0), L, L, plan, kf, work, stream, 0, 0, h0, H))) return rc;
+  return SFFFT_OK;
 }
 
 int sffft_spectrum_complex(const float* kr, const float* ki, int H, int L, const sffft_plan* plan, void* kf,
@@ -861,6 +924,7 @@ const char* sffft_strerror(int code) {
     case SFFFT_ENOPLAN: return "plan not compiled into this library";
     case SFFFT_EHIP: return "HIP runtime error";
     case SFFFT_ENOTFOUND: return "not found";
+    case SFFFT_ESCRATCH: return "the call needs more workspace than the library's static scratch holds";
     default: return "unknown error";
   }
 }
