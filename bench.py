@@ -51,6 +51,9 @@ def parse():
     ap.add_argument("--mode", type=int, default=None, help="0: workgroup per transform, 1: wavefront per pair")
     ap.add_argument("--channels", type=int, default=None, help="mode 1: channels per workgroup")
     ap.add_argument("--acc", type=int, default=0)
+    ap.add_argument("--gpu-warm-ms", type=float, default=300.0,
+                    help="before the timed steps, replay the captured steps for about this long so the GPU "
+                         "runs at its steady clocks (untimed)")
     ap.add_argument("--rotate-mb", type=float, default=600.0,
                     help="minimum total size of the rotated buffer sets (0 = one warm set)")
     ap.add_argument("--sweep", type=int, default=1,
@@ -196,10 +199,11 @@ def make_workload(sf, torch, dev, B, H, L, io, plan, rotate_mb, seed=0):
     return sets, decay, set_bytes
 
 
-def time_fused(sf, torch, cover, sets, plan, steps, warmup, work=None, warm=True):
+def time_fused(sf, torch, cover, sets, plan, steps, warmup, work=None, warm=True, gpu_warm_ms=0.0):
     """ms per step of K graph-replayed steps over the rotated sets; also the same steps
     launched eagerly, the warm single-set time, and whether the replay reproduced the
-    eager outputs bit for bit."""
+    eager outputs bit for bit. Before the timed replay the captured steps are replayed,
+    untimed, for about gpu_warm_ms, so the GPU leaves its idle clocks first."""
     nsets = len(sets)
 
     def step(i):
@@ -217,6 +221,10 @@ def time_fused(sf, torch, cover, sets, plan, steps, warmup, work=None, warm=True
         for i in range(steps):
             step(i)
     graph.replay()  # untimed replay
+    t_warm = time.perf_counter()
+    while (time.perf_counter() - t_warm) * 1e3 < gpu_warm_ms:
+        graph.replay()
+        torch.cuda.synchronize()
     host = host_time_ms(graph.replay)
     exact = all(torch.equal(s["y"], y0) for s, y0 in zip(sets, y_eager))
     ms = events_ms(cover, graph.replay, steps, host)
@@ -302,7 +310,8 @@ def sweep(a, sf, torch, np, dev, cover):
             t0 = time.perf_counter()
             plan = sf.default_plan(L, io, B)
             sets, _, set_bytes = make_workload(sf, torch, dev, B, H, L, io, plan, a.rotate_mb)
-            ms, _, ms_warm, exact, step = time_fused(sf, torch, cover, sets, plan, a.steps, 3, warm=True)
+            ms, _, ms_warm, exact, step = time_fused(sf, torch, cover, sets, plan, a.steps, 3, warm=True,
+                                                     gpu_warm_ms=min(a.gpu_warm_ms, 50.0))
             ms_ref = reference_protocol_ms(cover, lambda: step(0), L)
             s_io = 4 if io == "fp32" else 2
             algo = B * H * L * 2 * s_io + H * 2 * L * 8
@@ -400,7 +409,8 @@ def main():
     # graph is replayed between two events on the replay stream, behind a spin kernel
     # that covers the host's enqueue time. The same K steps launched eagerly are timed
     # beside it, and the same K steps on one buffer set (warm).
-    ms, ms_eager, ms_warm, replay_exact, step = time_fused(sf, torch, cover, sets, plan, a.steps, a.warmup, work)
+    ms, ms_eager, ms_warm, replay_exact, step = time_fused(sf, torch, cover, sets, plan, a.steps, a.warmup, work,
+                                                           gpu_warm_ms=a.gpu_warm_ms)
 
     # dispatch floor: a body-less kernel with the same grid, block and LDS size, K
     # launches replayed as a graph like the convolution (first call eager: it sets the
@@ -485,7 +495,9 @@ def main():
         "ms_dispatch_floor": None if ms_floor is None else round(ms_floor, 6),
         "io_only_frac": round(B * H * L * 2 * s_io / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
         "timing": ("HIP graph of the K steps replayed between events behind a spin kernel that covers the "
-                   "host enqueue; ms_eager: the same steps launched one by one"),
+                   "host enqueue, after W eager warmup steps and untimed replays for gpu_warm_ms; ms_eager: the "
+                   "same steps launched one by one"),
+        "gpu_warm_ms": a.gpu_warm_ms,
         "graph_replay_bitexact": bool(replay_exact),
         "rel_l2_vs_fp64": rel_err,
         "rel_l2_outputs": "all B*H*L" if L <= 16384 else "32 sampled sequences",

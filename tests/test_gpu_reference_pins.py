@@ -11,8 +11,8 @@ driver (`sffft`, the reference's CLI) on the reference's own input generator
   sequence), and the three-stage plans feed the fp32 input as an fp16 value plus its
   remainder (lower error); both are held to [0.75, 1.5] of the published value. bf16 I/O
   errors are dominated by the I/O rounding and must land within 25% in every case.
-- the north_star speed target: the selected fused candidate at least 4x faster than the
-  rocFFT pad/R2C/multiply/C2R/slice pipeline at every L of the reference's sweep
+- the speed target of the fused kernel: the selected fused candidate at least 4x faster than
+  the rocFFT pad/R2C/multiply/C2R/slice pipeline at every L of the reference's sweep
   (src/sffft.cu:372-381,506-513), for fp32 and bf16 I/O.
 """
 import csv
