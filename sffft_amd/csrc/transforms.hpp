@@ -2,9 +2,10 @@
 //
 // The reference lists standalone forward/inverse FFTs and 2-D convolution as not
 // exposed (README.md:174); these have no counterpart there. They favour accuracy over
-// speed: each stage is a dense radix-R DFT along one digit of the position, evaluated
-// in fp64 with exact fp64 twiddles and stored as complex64 between stages (relative
-// error ~1e-7). The fused convolution kernels, with fp16 MFMA operands, are separate.
+// speed: each stage is a radix-R DFT along one digit of the position, evaluated in fp64
+// (an in-register radix-2 FFT of the R points per thread, fp64 twiddles) and stored as
+// complex64 between stages (relative error ~1e-7). The fused convolution kernels, with
+// fp16 MFMA operands, are separate.
 //
 // Algorithm: N = r[0] * r[1] * ... * r[S-1] (powers of two, 16s first). Decimation in
 // frequency: stage J transforms digit J (stride s_J = r[J+1] * ... * r[S-1]) and, before
@@ -115,23 +116,62 @@ __global__ void __launch_bounds__(128)
   }
   float2* dst = out + q.base(s);
   const int Nj = R * sJ;
-  for (int k = 0; k < R; k++) {
-    double ar = 0.0, ai = 0.0;
+  // The line's DFT in registers: radix-2 decimation in frequency over log2(R) levels,
+  // natural input order, bit-reversed output order; fp64, twiddles w_R^e from the table.
+  // About R*log2(R)/2 complex products instead of the R*R of the dense sum.
+  double vr[R], vi[R];
 #pragma unroll
-    for (int t = 0; t < R; t++) {
-      const int e = (t * k) & (R - 1);
-      const double c = wc[e], sn = ws[e];
-      ar += (double)x[t].x * c - (double)x[t].y * sn;
-      ai += (double)x[t].x * sn + (double)x[t].y * c;
+  for (int t = 0; t < R; t++) {
+    vr[t] = (double)x[t].x;
+    vi[t] = (double)x[t].y;
+  }
+#pragma unroll
+  for (int m = R; m >= 2; m >>= 1) {
+    const int h = m >> 1, step = R / m;  // w_m^j = w_R^(j * step)
+#pragma unroll
+    for (int b = 0; b < R; b += m)
+#pragma unroll
+      for (int j = 0; j < h; j++) {
+        const int i0 = b + j, i1 = i0 + h;
+        const double ar = vr[i0], ai = vi[i0], dr = ar - vr[i1], di = ai - vi[i1];
+        vr[i0] = ar + vr[i1];
+        vi[i0] = ai + vi[i1];
+        if (j == 0) {
+          vr[i1] = dr;
+          vi[i1] = di;
+        } else {
+          const double c = wc[j * step], sn = ws[j * step];
+          vr[i1] = dr * c - di * sn;
+          vi[i1] = dr * sn + di * c;
+        }
+      }
+  }
+  auto bitrev = [](int k) {
+    int r = 0;
+#pragma unroll
+    for (int b = 1; b < R; b <<= 1) r = (r << 1) | ((k & b) ? 1 : 0);
+    return r;
+  };
+  if (last) {
+#pragma unroll
+    for (int k = 0; k < R; k++) {
+      const int r = bitrev(k);
+      dst[(kbase + (long long)k * wlast) * q.stride] = make_float2((float)(vr[r] * scale), (float)(vi[r] * scale));
     }
-    if (last) {
-      dst[(kbase + (long long)k * wlast) * q.stride] = make_float2((float)(ar * scale), (float)(ai * scale));
-    } else {
-      const int e = (int)(((long long)k * inner) % Nj);
-      double sn, c;
-      sincospi(2.0 * (double)e / (double)Nj, &sn, &c);
-      sn *= sign;
-      work[widx(base + k * sJ)] = make_float2((float)(ar * c - ai * sn), (float)(ar * sn + ai * c));
+  } else {
+    // twiddle w_Nj^(k * inner) before the next stage: powers of w_Nj^inner, in fp64
+    double w1s, w1c;
+    sincospi(2.0 * (double)inner / (double)Nj, &w1s, &w1c);
+    w1s *= sign;
+    double wr = 1.0, wi = 0.0;
+#pragma unroll
+    for (int k = 0; k < R; k++) {
+      const int r = bitrev(k);
+      work[widx(base + k * sJ)] =
+          make_float2((float)(vr[r] * wr - vi[r] * wi), (float)(vr[r] * wi + vi[r] * wr));
+      const double nr = wr * w1c - wi * w1s;
+      wi = wr * w1s + wi * w1c;
+      wr = nr;
     }
   }
 }
