@@ -530,15 +530,16 @@ class RocfftPipeline:
             self.h = ctypes.c_void_p()
 
 
-# Sources that determine the kernels' machine code: a profile summary measured on a
-# build of other sources does not describe this one.
-KERNEL_SOURCES = ("csrc/fftconv.hpp", "csrc/fftconv_wave.hpp", "csrc/longconv.hpp", "csrc/transforms.hpp",
-                  "csrc/registry.hpp", "csrc/plans.def", "csrc/conv_inst.hip", "csrc/long_inst.hip", "csrc/api.hip",
-                  "Makefile")
+# Sources the convolution kernels (wave pipeline, workgroup kernel, multi-pass passes) are
+# compiled from, with the build flags: a profile summary measured on a build of other
+# sources does not describe this one. (The host code, the spectrum preparation and the
+# standalone transforms, in api.hip and transforms.hpp, are not part of those kernels.)
+KERNEL_SOURCES = ("csrc/fftconv.hpp", "csrc/fftconv_wave.hpp", "csrc/longconv.hpp", "csrc/registry.hpp",
+                  "csrc/plans.def", "csrc/conv_inst.hip", "csrc/long_inst.hip", "Makefile")
 
 
 def kernel_sources_sha() -> str:
-    """First 16 hex digits of the sha256 over the kernel sources and build flags."""
+    """First 16 hex digits of the sha256 over the convolution kernels' sources and build flags."""
     import hashlib
 
     h = hashlib.sha256()
