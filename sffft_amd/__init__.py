@@ -180,9 +180,9 @@ DEFAULT_PLANS = {
     (512, "fp32"): ("32x32", 4, 2, 1, 1), (512, "bf16"): ("32x32", 4, 2, 1, 1),
     (1024, "fp32"): ("64x32", 12, 2, 1, 3), (1024, "bf16"): ("64x32", 12, 2, 1, 3),
     (2048, "fp32"): ("64x64", 12, 2, 1, 3), (2048, "bf16"): ("64x64", 12, 2, 1, 3),
-    (4096, "fp32"): ("32x16x16", 8, 2, 0, 1), (4096, "bf16"): ("32x16x16", 8, 2, 0, 1),
-    (8192, "fp32"): ("32x32x16", 8, 2, 0, 1), (8192, "bf16"): ("64x16x16", 8, 2, 0, 1),
-    (16384, "fp32"): ("32x32x32", 16, 2, 0, 1), (16384, "bf16"): ("32x32x32", 16, 2, 0, 1),
+    (4096, "fp32"): ("32x16x16", 4, 2, 0, 1), (4096, "bf16"): ("32x16x16", 4, 2, 0, 1),
+    (8192, "fp32"): ("32x32x16", 8, 2, 0, 1), (8192, "bf16"): ("32x32x16", 8, 2, 0, 1),
+    (16384, "fp32"): ("32x32x32", 8, 2, 0, 1), (16384, "bf16"): ("32x32x32", 8, 2, 0, 1),
 }
 # Multi-pass plans (mode 2): column radix x row plan, measured at B=8, H=768
 LONG_DEFAULT_PLANS = {32768: "64x32x32", 65536: "64x64x32", 131072: "64x64x64"}

@@ -10,13 +10,30 @@
 
 namespace sffft {
 
+// Register budget of a workgroup-kernel plan (wavefronts per SIMD the allocation must
+// allow; 1: the compiler's own). 64x16x16 with 8 wavefronts and table fragments is held
+// to the occupancy its 80 KB of LDS allows (two workgroups per CU, 128 VGPRs): left
+// alone it takes 147-156 VGPRs and loses a workgroup per CU (measured 10% slower). Held
+// to their LDS-limited occupancy the other plans (and this one with in-kernel
+// fragments) spill, or gain nothing.
+template <class P, int NW, bool CACHED>
+constexpr int fused_wpe() {
+  return CACHED && P::R0 == 64 && P::R1 == 16 && P::R2 == 16 && NW == 8 ? lds_waves_per_simd<P, NW>() : 1;
+}
+
 template <class P, int NW, int NSEQ, class TIO, bool CACHED>
 static hipError_t launch_fused(const void* u, const void* kf, void* y, int B, int H, const void* ftab, const void*,
                                int acc16, hipStream_t stream) {
   const unsigned grid = (unsigned)(H * (B / NSEQ));
-  hipLaunchKernelGGL((fftconv_kernel<P, NW, NSEQ, TIO, CACHED>), dim3(grid), dim3(64 * NW), 0, stream,
-                     static_cast<const TIO*>(u), static_cast<const float2*>(kf), static_cast<TIO*>(y), B, H,
-                     static_cast<const h8*>(ftab), acc16);
+  constexpr int WPE = fused_wpe<P, NW, CACHED>();
+  if (acc16)
+    hipLaunchKernelGGL((fftconv_kernel<P, NW, NSEQ, TIO, CACHED, true, WPE>), dim3(grid), dim3(64 * NW), 0, stream,
+                       static_cast<const TIO*>(u), static_cast<const float2*>(kf), static_cast<TIO*>(y), B, H,
+                       static_cast<const h8*>(ftab));
+  else
+    hipLaunchKernelGGL((fftconv_kernel<P, NW, NSEQ, TIO, CACHED, false, WPE>), dim3(grid), dim3(64 * NW), 0, stream,
+                       static_cast<const TIO*>(u), static_cast<const float2*>(kf), static_cast<TIO*>(y), B, H,
+                       static_cast<const h8*>(ftab));
   return hipGetLastError();
 }
 
@@ -52,10 +69,10 @@ static Entry make_entry() {
   Entry e = {SFFFT_INST_L, A, B_, C_, W, S, 0, 1, P::LDS_BYTES,
              {{&launch_fused<P, W, S, float, false>, &launch_fused<P, W, S, float, true>},
               {&launch_fused<P, W, S, uint16_t, false>, &launch_fused<P, W, S, uint16_t, true>}},
-             {{reinterpret_cast<const void*>(&fftconv_kernel<P, W, S, float, false>),
-               reinterpret_cast<const void*>(&fftconv_kernel<P, W, S, float, true>)},
-              {reinterpret_cast<const void*>(&fftconv_kernel<P, W, S, uint16_t, false>),
-               reinterpret_cast<const void*>(&fftconv_kernel<P, W, S, uint16_t, true>)}},
+             {{reinterpret_cast<const void*>(&fftconv_kernel<P, W, S, float, false, false, fused_wpe<P, W, false>()>),
+               reinterpret_cast<const void*>(&fftconv_kernel<P, W, S, float, true, false, fused_wpe<P, W, true>()>)},
+              {reinterpret_cast<const void*>(&fftconv_kernel<P, W, S, uint16_t, false, false, fused_wpe<P, W, false>()>),
+               reinterpret_cast<const void*>(&fftconv_kernel<P, W, S, uint16_t, true, false, fused_wpe<P, W, true>()>)}},
              {{nullptr, nullptr}, {nullptr, nullptr}}};
   return e;
 }

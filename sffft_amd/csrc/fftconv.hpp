@@ -884,12 +884,24 @@ __device__ __forceinline__ void block_to_item(int i, int H, int BP, int& h, int&
   }
 }
 
+// Wavefronts per SIMD that the workgroup's LDS allows on one CU (160 KB), at most 8.
+template <class P, int NW>
+__host__ __device__ constexpr int lds_waves_per_simd() {
+  return (163840 / P::LDS_BYTES) * NW / 4 < 1 ? 1 : (163840 / P::LDS_BYTES) * NW / 4 > 8 ? 8 : (163840 / P::LDS_BYTES) * NW / 4;
+}
+
 // grid = H * (B / NSEQ) workgroups of 64*NW lanes; one sequence (NSEQ = 1) or one
 // pair of sequences of the same channel (NSEQ = 2) per workgroup.
-template <class P, int NW, int NSEQ, class TIO, bool CACHED>
-__global__ void __launch_bounds__(64 * NW)
+// ACC16 (fp16-accumulation mode) is a compile-time choice: as a runtime flag every
+// accumulator rounding was a branch, and the branches cut each phase into one
+// scheduling block per tile. WPE is the wavefronts per SIMD the register allocation
+// must allow (the LDS-limited occupancy, or 1 for no limit): without it the schedule
+// of the longer blocks can take more VGPRs than that occupancy leaves.
+template <class P, int NW, int NSEQ, class TIO, bool CACHED, bool ACC16, int WPE>
+__global__ void __launch_bounds__(64 * NW, WPE)
     fftconv_kernel(const TIO* __restrict__ u, const float2* __restrict__ kf, TIO* __restrict__ y, int B, int H,
-                   const h8* __restrict__ ftab, int acc16) {
+                   const h8* __restrict__ ftab) {
+  constexpr int acc16 = ACC16 ? 1 : 0;
   __shared__ __attribute__((aligned(16))) _Float16 lds[2 * P::PLANE];
   _Float16* re = lds;
   _Float16* im = lds + P::PLANE;

@@ -3,9 +3,11 @@
 - B=8, H=768, L=1024, 64x32 (wave pipeline, the benchmark workload), fp32 and bf16 I/O;
 - B=8, H=768, L=2048: 16x16x16 with bf16 I/O, fp32 and fp16 accumulation, and the
   default 64x64 wave plan in both I/O types;
-- B=8, H=768, L=8192: 32x32x16 in fp32 and bf16 I/O and the default bf16 plan 64x16x16;
-- B=4, H=1536, L=16384, 32x32x32 in bf16 (and fp32) I/O, a long filter made of 16
-  decaying sinusoids per channel.
+- B=8, H=768, L=4096: the default plan 32x16x16 with 4 wavefronts, fp32 and bf16 I/O;
+- B=8, H=768, L=8192: 32x32x16 (the default, 8 wavefronts, and 4) in fp32 and bf16 I/O,
+  and 64x16x16 (held to 128 VGPRs) in bf16;
+- B=4, H=1536, L=16384, 32x32x32 (the default, 8 wavefronts, and 16) in bf16 and fp32
+  I/O, a long filter made of 16 decaying sinusoids per channel.
 
 Every B*H*L output is compared with the fp64 oracle (src/sffft.cu:394-399): the direct
 convolution up to L=2048, the fp64 FFT convolution above it, itself cross-checked
@@ -80,9 +82,12 @@ CONFIGS = [
     (8, 768, 1024, "decay256", [("64x32", 12, 2, 1, 3, 0, ("fp32", "bf16"))]),
     (8, 768, 2048, "decay256", [("16x16x16", 4, 2, 0, 1, 0, ("bf16",)), ("16x16x16", 4, 2, 0, 1, 1, ("bf16",)),
                                 ("64x64", 12, 2, 1, 3, 0, ("fp32", "bf16"))]),
-    (8, 768, 8192, "decay2048", [("32x32x16", 4, 2, 0, 1, 0, ("fp32", "bf16")),
+    (8, 768, 4096, "decay2048", [("32x16x16", 4, 2, 0, 1, 0, ("fp32", "bf16"))]),
+    (8, 768, 8192, "decay2048", [("32x32x16", 8, 2, 0, 1, 0, ("fp32", "bf16")),
+                                 ("32x32x16", 4, 2, 0, 1, 0, ("fp32", "bf16")),
                                  ("64x16x16", 8, 2, 0, 1, 0, ("bf16",))]),
-    (4, 1536, 16384, "sines", [("32x32x32", 16, 2, 0, 1, 0, ("bf16", "fp32"))]),
+    (4, 1536, 16384, "sines", [("32x32x32", 8, 2, 0, 1, 0, ("bf16", "fp32")),
+                               ("32x32x32", 16, 2, 0, 1, 0, ("bf16", "fp32"))]),
 ]
 
 
