@@ -133,30 +133,49 @@ __global__ void __launch_bounds__(64 * LC_WAVES)
   const int r = lane & 15, g = lane >> 4;
   const int N = NC * NR, LEN = CIRC ? N : N / 2;  // row length of u and y
   const ColBlock cbk = col_block(B, H, LEN, NR, pi0, wave);
-  const bool live = CIRC || NC >= 32 || g < 2;  // NC = 16: rows n1 >= 8 are the zero padding
-
-  TIO raw[MT][KS][8];
+  // The wavefront's block, rows n1 < NZ of both sequences and LC_COLS columns, is read
+  // as 16-byte row chunks (whole 128-byte lines, CPR lanes per row), every load issued
+  // before the first is used; then, one K step at a time, the chunks go through the
+  // wavefront's LDS scratch into the operand layout (lane (r, g): column 16mt + r, rows
+  // 16ks + 4g + j). The scratch rows are 16 bytes longer than the block, which puts the
+  // four lane groups' rows on different banks.
+  constexpr int NZ = CIRC ? NC : NC / 2;  // non-zero rows n1 (the rest is the zero padding)
+  constexpr int KR = NZ < 16 ? NZ : 16;   // non-zero rows per K step and sequence
+  constexpr int EPC = 16 / (int)sizeof(TIO), CPR = LC_COLS / EPC, PITCH = LC_COLS + EPC;
+  constexpr int LPK = 2 * KR * CPR / 64;  // load instructions per K step
+  static_assert(2 * KR * CPR % 64 == 0 && KS * KR == NZ, "whole load rounds per K step");
+  __shared__ __attribute__((aligned(16))) TIO scratch[LC_WAVES][2 * KR * PITCH];
+  TIO* S = scratch[wave];
+  u32x4 c[KS][LPK];
 #pragma unroll
-  for (int mt = 0; mt < MT; mt++)
+  for (int ks = 0; ks < KS; ks++)
 #pragma unroll
-    for (int ks = 0; ks < KS; ks++)
-#pragma unroll
-      for (int j = 0; j < 8; j++) {
-        const size_t off = (size_t)(16 * ks + 4 * g + (j & 3)) * NR + cbk.cb + 16 * mt + r;
-        raw[mt][ks][j] = live ? u[(j < 4 ? cbk.ra : cbk.rb) + off] : (TIO)0;
-      }
+    for (int i = 0; i < LPK; i++) {
+      const int q = i * 64 + lane, row = q / CPR, seq = row / KR;
+      const size_t off = (size_t)(16 * ks + row - seq * KR) * NR + cbk.cb + (q % CPR) * EPC;
+      c[ks][i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(u + (seq ? cbk.rb : cbk.ra) + off));
+    }
   h8 ah[MT][KS], al[SPLIT ? MT : 1][KS];
 #pragma unroll
-  for (int mt = 0; mt < MT; mt++)
+  for (int ks = 0; ks < KS; ks++) {
 #pragma unroll
-    for (int ks = 0; ks < KS; ks++)
+    for (int i = 0; i < LPK; i++) {
+      const int q = i * 64 + lane;
+      *reinterpret_cast<u32x4*>(S + (q / CPR) * PITCH + (q % CPR) * EPC) = c[ks][i];
+    }
+    wave_lds_fence();  // other lanes' chunks are read below
+#pragma unroll
+    for (int mt = 0; mt < MT; mt++)
 #pragma unroll
       for (int j = 0; j < 8; j++) {
-        const float x = io_to_f32(raw[mt][ks][j]);
+        const int row = 4 * g + (j & 3);
+        const float x = row < KR ? io_to_f32(S[((j < 4 ? 0 : KR) + row) * PITCH + 16 * mt + r]) : 0.f;
         const _Float16 hi = (_Float16)x;
         ah[mt][ks][j] = hi;
         if constexpr (SPLIT) al[mt][ks][j] = (_Float16)(x - (float)hi);
       }
+    wave_lds_fence();  // every lane has read the block before the next K step overwrites it
+  }
 
   uint32_t* T = work + (size_t)cbk.slot * N;
 #pragma unroll
