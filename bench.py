@@ -463,7 +463,7 @@ def main():
         cpu = cpu_baseline(oracle, np, u32_np, k_np, B, H, L, a.cpu_seconds, oracle.threads())
         cpu1 = cpu_baseline(oracle, np, u32_np, k_np, B, H, L, a.cpu_seconds, 1)
 
-    stamp = sf.kernel_sources_sha()
+    stamp = sf.kernel_sources_sha(plan.mode)
     out = {
         "metric": "ms per B=8xH=768 batch vs L (fp32/bf16 I/O); % HBM roofline; rel L2 err",
         "value": round(ms, 6),

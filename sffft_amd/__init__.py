@@ -534,16 +534,21 @@ class RocfftPipeline:
 # compiled from, with the build flags: a profile summary measured on a build of other
 # sources does not describe this one. (The host code, the spectrum preparation and the
 # standalone transforms, in api.hip and transforms.hpp, are not part of those kernels.)
-KERNEL_SOURCES = ("csrc/fftconv.hpp", "csrc/fftconv_wave.hpp", "csrc/longconv.hpp", "csrc/registry.hpp",
-                  "csrc/plans.def", "csrc/conv_inst.hip", "csrc/long_inst.hip", "Makefile")
+# The sources each kernel family is compiled from, and the build flags (Makefile): the
+# single-pass kernels (plan modes 0 and 1, conv_inst.hip) and the multi-pass kernels
+# (mode 2, long_inst.hip, which also include the single-pass headers).
+SINGLE_PASS_SOURCES = ("csrc/fftconv.hpp", "csrc/fftconv_wave.hpp", "csrc/registry.hpp", "csrc/plans.def",
+                       "csrc/conv_inst.hip", "Makefile")
+MULTI_PASS_SOURCES = SINGLE_PASS_SOURCES + ("csrc/longconv.hpp", "csrc/long_inst.hip")
 
 
-def kernel_sources_sha() -> str:
-    """First 16 hex digits of the sha256 over the convolution kernels' sources and build flags."""
+def kernel_sources_sha(mode: int = 1) -> str:
+    """First 16 hex digits of the sha256 over the sources and build flags of the kernel
+    family that runs plans of this mode (0 and 1: single-pass, 2: multi-pass)."""
     import hashlib
 
     h = hashlib.sha256()
-    for rel in KERNEL_SOURCES:
+    for rel in MULTI_PASS_SOURCES if mode == 2 else SINGLE_PASS_SOURCES:
         with open(os.path.join(_HERE, rel), "rb") as f:
             h.update(rel.encode() + b"\0" + f.read() + b"\0")
     return h.hexdigest()[:16]
