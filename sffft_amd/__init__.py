@@ -542,15 +542,29 @@ SINGLE_PASS_SOURCES = ("csrc/fftconv.hpp", "csrc/fftconv_wave.hpp", "csrc/regist
 MULTI_PASS_SOURCES = SINGLE_PASS_SOURCES + ("csrc/longconv.hpp", "csrc/long_inst.hip")
 
 
+def _code_only(rel: str, text: str) -> str:
+    """The source without its comments (C++ // and /* */, Makefile #), blank lines and
+    indentation, so that an edit of comments or layout does not change the stamp of an
+    unchanged kernel."""
+    import re
+
+    if rel.endswith("Makefile"):
+        text = re.sub(r"(?m)^\s*#.*$", "", text)
+    else:
+        text = re.sub(r"//[^\n]*", "", re.sub(r"/\*.*?\*/", "", text, flags=re.S))
+    return "\n".join(line.strip() for line in text.splitlines() if line.strip())
+
+
 def kernel_sources_sha(mode: int = 1) -> str:
-    """First 16 hex digits of the sha256 over the sources and build flags of the kernel
-    family that runs plans of this mode (0 and 1: single-pass, 2: multi-pass)."""
+    """First 16 hex digits of the sha256 over the code (comments removed) of the sources
+    and build flags of the kernel family that runs plans of this mode (0 and 1:
+    single-pass, 2: multi-pass)."""
     import hashlib
 
     h = hashlib.sha256()
     for rel in MULTI_PASS_SOURCES if mode == 2 else SINGLE_PASS_SOURCES:
-        with open(os.path.join(_HERE, rel), "rb") as f:
-            h.update(rel.encode() + b"\0" + f.read() + b"\0")
+        with open(os.path.join(_HERE, rel)) as f:
+            h.update(rel.encode() + b"\0" + _code_only(rel, f.read()).encode() + b"\0")
     return h.hexdigest()[:16]
 
 
