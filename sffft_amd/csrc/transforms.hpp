@@ -11,7 +11,9 @@
 // frequency: stage J transforms digit J (stride s_J = r[J+1] * ... * r[S-1]) and, before
 // the next stage, multiplies by w_{r[J] s_J}^(k_J * (p mod s_J)). After the last stage
 // position p = sum_J k_J s_J holds frequency k = k_0 + r[0] (k_1 + r[1] (k_2 + ...)), so
-// the last stage writes each value to its natural-order slot directly.
+// the last stage writes each value to its natural-order slot directly. Contiguous sequences
+// of up to ONEPASS_MAX_N points run every stage in LDS in one launch (line_kernel); longer
+// or strided ones take one launch per stage (stage_kernel), through a workspace.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -69,6 +71,67 @@ struct Seqs {
   }
 };
 
+// The radix-R DFT of one line's R points, in registers, shared by both kernels below:
+// radix-2 decimation in frequency over log2(R) levels, natural input order, bit-reversed
+// output order, in fp64 with w_m^j = w_T^(j * T / m) read from a table of the T-th roots
+// of unity. About R*log2(R)/2 complex products instead of the R*R of the dense sum.
+// Contraction is off and the complex products are written with fma, so every kernel
+// that inlines this rounds in the same places and gets the same bits.
+template <int R, int T>
+__device__ __forceinline__ void line_dft(double (&vr)[R], double (&vi)[R], const double* wc, const double* ws) {
+#pragma clang fp contract(off)
+#pragma unroll
+  for (int m = R; m >= 2; m >>= 1) {
+    const int h = m >> 1, step = T / m;
+#pragma unroll
+    for (int b = 0; b < R; b += m)
+#pragma unroll
+      for (int j = 0; j < h; j++) {
+        const int i0 = b + j, i1 = i0 + h;
+        const double ar = vr[i0], ai = vi[i0], dr = ar - vr[i1], di = ai - vi[i1];
+        vr[i0] = ar + vr[i1];
+        vi[i0] = ai + vi[i1];
+        if (j == 0) {
+          vr[i1] = dr;
+          vi[i1] = di;
+        } else {
+          const double c = wc[j * step], sn = ws[j * step];
+          vr[i1] = fma(dr, c, -(di * sn));
+          vi[i1] = fma(dr, sn, di * c);
+        }
+      }
+  }
+}
+
+template <int R>
+__device__ __forceinline__ int bitrev(int k) {
+  int r = 0;
+#pragma unroll
+  for (int b = 1; b < R; b <<= 1) r = (r << 1) | ((k & b) ? 1 : 0);
+  return r;
+}
+
+// Frequency digit k of a non-last stage's line times w_Nj^(k * inner), rounded to
+// complex64 once; store(k, value) for k = 0 .. R-1. The twiddles are powers of
+// w_Nj^inner, built by recurrence in fp64 (same rounding rule as line_dft).
+template <int R, class Store>
+__device__ __forceinline__ void twiddled_outputs(const double (&vr)[R], const double (&vi)[R], int inner, int Nj,
+                                                 int sign, Store store) {
+#pragma clang fp contract(off)
+  double w1s, w1c;
+  sincospi(2.0 * (double)inner / (double)Nj, &w1s, &w1c);
+  w1s *= sign;
+  double wr = 1.0, wi = 0.0;
+#pragma unroll
+  for (int k = 0; k < R; k++) {
+    const int r = bitrev<R>(k);
+    store(k, make_float2((float)fma(vr[r], wr, -(vi[r] * wi)), (float)fma(vr[r], wi, vi[r] * wr)));
+    const double nr = fma(wr, w1c, -(wi * w1s));
+    wi = fma(wr, w1s, wi * w1c);
+    wr = nr;
+  }
+}
+
 template <int R>
 __global__ void __launch_bounds__(128)
     stage_kernel(const float2* in, float2* out, float2* work, Seqs q, Radices d, int J, int N, int sign,
@@ -116,63 +179,149 @@ __global__ void __launch_bounds__(128)
   }
   float2* dst = out + q.base(s);
   const int Nj = R * sJ;
-  // The line's DFT in registers: radix-2 decimation in frequency over log2(R) levels,
-  // natural input order, bit-reversed output order; fp64, twiddles w_R^e from the table.
-  // About R*log2(R)/2 complex products instead of the R*R of the dense sum.
   double vr[R], vi[R];
 #pragma unroll
   for (int t = 0; t < R; t++) {
     vr[t] = (double)x[t].x;
     vi[t] = (double)x[t].y;
   }
-#pragma unroll
-  for (int m = R; m >= 2; m >>= 1) {
-    const int h = m >> 1, step = R / m;  // w_m^j = w_R^(j * step)
-#pragma unroll
-    for (int b = 0; b < R; b += m)
-#pragma unroll
-      for (int j = 0; j < h; j++) {
-        const int i0 = b + j, i1 = i0 + h;
-        const double ar = vr[i0], ai = vi[i0], dr = ar - vr[i1], di = ai - vi[i1];
-        vr[i0] = ar + vr[i1];
-        vi[i0] = ai + vi[i1];
-        if (j == 0) {
-          vr[i1] = dr;
-          vi[i1] = di;
-        } else {
-          const double c = wc[j * step], sn = ws[j * step];
-          vr[i1] = dr * c - di * sn;
-          vi[i1] = dr * sn + di * c;
-        }
-      }
-  }
-  auto bitrev = [](int k) {
-    int r = 0;
-#pragma unroll
-    for (int b = 1; b < R; b <<= 1) r = (r << 1) | ((k & b) ? 1 : 0);
-    return r;
-  };
+  line_dft<R, R>(vr, vi, wc, ws);
   if (last) {
 #pragma unroll
     for (int k = 0; k < R; k++) {
-      const int r = bitrev(k);
+      const int r = bitrev<R>(k);
       dst[(kbase + (long long)k * wlast) * q.stride] = make_float2((float)(vr[r] * scale), (float)(vi[r] * scale));
     }
   } else {
-    // twiddle w_Nj^(k * inner) before the next stage: powers of w_Nj^inner, in fp64
-    double w1s, w1c;
-    sincospi(2.0 * (double)inner / (double)Nj, &w1s, &w1c);
-    w1s *= sign;
-    double wr = 1.0, wi = 0.0;
+    // twiddle w_Nj^(k * inner) before the next stage
+    twiddled_outputs<R>(vr, vi, inner, Nj, sign, [&](int k, float2 v) { work[widx(base + k * sJ)] = v; });
+  }
+}
+
+// ---- one pass over short contiguous lines ------------------------------------------
+// Sequences of N <= ONEPASS_MAX_N elements at unit stride are transformed in one launch: a
+// workgroup loads G = max(1, ONEPASS_SLOTS / N) whole sequences into LDS, runs every stage
+// there and writes the natural-order result back, so each sequence crosses HBM once
+// each way instead of once per stage. The stages are those of stage_kernel (the same
+// radix split, fp64 line DFTs, twiddle recurrences and complex64 rounding between
+// stages), so the results are bit-identical to the staged path. One LDS slot of padding
+// per 16 elements keeps the threads of the last stage (R consecutive elements each) on
+// different banks.
+constexpr int ONEPASS_MAX_N = 8192;
+constexpr int ONEPASS_SLOTS = 4096;
+constexpr int ONEPASS_THREADS = 256;
+
+__device__ __forceinline__ int lpad(int p) { return p + (p >> 4); }
+
+template <int N>
+struct LineGeom {
+  static constexpr int G = N >= ONEPASS_SLOTS ? 1 : ONEPASS_SLOTS / N;  // sequences per workgroup
+  static constexpr int SLOTS = G * N;
+  static constexpr int LDS = SLOTS + SLOTS / 16;
+  // radix of the stage whose remaining product of radices is REST (16s first)
+  static constexpr int radix(int rest) { return rest > MAX_RADIX ? MAX_RADIX : rest; }
+};
+
+// One stage over the workgroup's lines: REST is the product of this and the later
+// radices (REST = N at the first stage), R this stage's radix, sJ = REST / R its stride.
+template <int N, int REST>
+__device__ __forceinline__ void line_stage(float2* buf, const double* wc, const double* ws, int sign, float scale) {
+  constexpr int R = LineGeom<N>::radix(REST), sJ = REST / R, LPS = N / R;
+  constexpr int LINES = LineGeom<N>::G * LPS;
+  constexpr bool LAST = REST == R;
+  for (int li = threadIdx.x; li < LINES; li += ONEPASS_THREADS) {
+    const int g = li / LPS, l = li - g * LPS;
+    const int inner = l % sJ, base = g * N + (l / sJ) * REST + inner;
+    double vr[R], vi[R];
 #pragma unroll
-    for (int k = 0; k < R; k++) {
-      const int r = bitrev(k);
-      work[widx(base + k * sJ)] =
-          make_float2((float)(vr[r] * wr - vi[r] * wi), (float)(vr[r] * wi + vi[r] * wr));
-      const double nr = wr * w1c - wi * w1s;
-      wi = wr * w1s + wi * w1c;
-      wr = nr;
+    for (int t = 0; t < R; t++) {
+      const float2 x = buf[lpad(base + t * sJ)];
+      vr[t] = (double)x.x;
+      vi[t] = (double)x.y;
     }
+    line_dft<R, MAX_RADIX>(vr, vi, wc, ws);
+    if constexpr (LAST) {
+      // in place, scaled: element base + k holds frequency digit k of this line
+#pragma unroll
+      for (int k = 0; k < R; k++) {
+        const int r = bitrev<R>(k);
+        buf[lpad(base + k)] = make_float2((float)(vr[r] * scale), (float)(vi[r] * scale));
+      }
+    } else {
+      twiddled_outputs<R>(vr, vi, inner, REST, sign, [&](int k, float2 v) { buf[lpad(base + k * sJ)] = v; });
+    }
+  }
+  __syncthreads();
+  if constexpr (!LAST) line_stage<N, REST / R>(buf, wc, ws, sign, scale);
+}
+
+// Position in the line, after the last stage, of natural-order frequency f: the digits
+// of f below the last stage's (f mod W, W the product of all radices but the last) name
+// the line, reversed into its base position; the last digit is the element within it.
+template <int N>
+__device__ __forceinline__ int line_position(int f) {
+  int W = 1, rest = N;
+  while (rest > MAX_RADIX) {
+    W *= MAX_RADIX;
+    rest /= MAX_RADIX;
+  }
+  int kb = f % W, base = 0, sj = N;
+  for (int w = 1; w < W; w *= MAX_RADIX) {
+    sj /= MAX_RADIX;
+    base += ((kb / w) % MAX_RADIX) * sj;
+  }
+  return base + f / W;
+}
+
+template <int N>
+__global__ void __launch_bounds__(ONEPASS_THREADS)
+    line_kernel(const float2* in, float2* out, Seqs q, int sign, float scale) {
+  typedef LineGeom<N> LG;
+  __shared__ float2 buf[LG::LDS];
+  __shared__ double wc[MAX_RADIX], ws[MAX_RADIX];
+  if (threadIdx.x < MAX_RADIX) {
+    double sn, c;
+    sincospi(2.0 * (double)threadIdx.x / (double)MAX_RADIX, &sn, &c);
+    wc[threadIdx.x] = c;
+    ws[threadIdx.x] = sign * sn;
+  }
+  const long long s0 = (long long)blockIdx.x * LG::G;
+  const int G = q.nseq - s0 < LG::G ? (int)(q.nseq - s0) : LG::G;
+  for (int i = threadIdx.x; i < LG::SLOTS; i += ONEPASS_THREADS) {
+    const int g = i / N;
+    buf[lpad(i)] = g < G ? in[q.base(s0 + g) + (i - g * N)] : make_float2(0.f, 0.f);
+  }
+  __syncthreads();
+  line_stage<N, N>(buf, wc, ws, sign, scale);
+  for (int i = threadIdx.x; i < G * N; i += ONEPASS_THREADS) {
+    const int g = i / N, f = i - g * N;
+    out[q.base(s0 + g) + f] = buf[lpad(g * N + line_position<N>(f))];
+  }
+}
+
+template <int N>
+inline void launch_line(const float2* in, float2* out, const Seqs& q, int sign, float scale, hipStream_t st) {
+  const unsigned grid = (unsigned)((q.nseq + LineGeom<N>::G - 1) / LineGeom<N>::G);
+  hipLaunchKernelGGL(line_kernel<N>, dim3(grid), dim3(ONEPASS_THREADS), 0, st, in, out, q, sign, scale);
+}
+
+inline bool run_lines(const float2* in, float2* out, const Seqs& q, int N, int sign, float scale, hipStream_t st) {
+  if (q.stride != 1 || q.seq_fast) return false;
+  switch (N) {
+    case 2: launch_line<2>(in, out, q, sign, scale, st); return true;
+    case 4: launch_line<4>(in, out, q, sign, scale, st); return true;
+    case 8: launch_line<8>(in, out, q, sign, scale, st); return true;
+    case 16: launch_line<16>(in, out, q, sign, scale, st); return true;
+    case 32: launch_line<32>(in, out, q, sign, scale, st); return true;
+    case 64: launch_line<64>(in, out, q, sign, scale, st); return true;
+    case 128: launch_line<128>(in, out, q, sign, scale, st); return true;
+    case 256: launch_line<256>(in, out, q, sign, scale, st); return true;
+    case 512: launch_line<512>(in, out, q, sign, scale, st); return true;
+    case 1024: launch_line<1024>(in, out, q, sign, scale, st); return true;
+    case 2048: launch_line<2048>(in, out, q, sign, scale, st); return true;
+    case 4096: launch_line<4096>(in, out, q, sign, scale, st); return true;
+    case 8192: launch_line<8192>(in, out, q, sign, scale, st); return true;
+    default: return false;
   }
 }
 
@@ -190,6 +339,7 @@ inline hipError_t run(const float2* in, float2* out, float2* work, const Seqs& q
   Radices d;
   if (!split(N, &d)) return hipErrorInvalidValue;
   const int sign = inverse ? 1 : -1;
+  if (N <= ONEPASS_MAX_N && run_lines(in, out, q, N, sign, scale, st)) return hipGetLastError();
   for (int J = 0; J < d.S; J++) {
     const long long threads = q.nseq * (N / d.r[J]);
     const dim3 grid((unsigned)((threads + 127) / 128)), block(128);

@@ -60,6 +60,21 @@ def test_fft_closed_forms(N):
     assert np.abs(Xi[0] - ei).max() <= 2e-6 * N
 
 
+@pytest.mark.parametrize("batch,N", [(3, 2), (64, 16), (9, 256), (5, 1024), (4, 2048), (3, 4096), (3, 8192)])
+def test_one_pass_matches_staged_path_bitwise(batch, N):
+    """Contiguous sequences of N <= 8192 take the one-pass kernel (every stage in LDS); the
+    same values as the columns of a matrix take the staged kernels. The stages do the
+    same arithmetic, so the two agree bit for bit, forward and inverse with a scale."""
+    print(f"one-pass vs staged batch={batch} N={N}", flush=True)
+    x = crandn(np.random.default_rng(3 * N + batch), batch, N)
+    rows = torch.from_numpy(x).to(DEV)
+    cols = torch.from_numpy(np.ascontiguousarray(x.T)).to(DEV)
+    for inverse, scale in ((False, 1.0), (True, 1.0 / N)):
+        a = sf.fft(rows, inverse=inverse, scale=scale).cpu().numpy()
+        b = np.ascontiguousarray(sf.fft(cols, inverse=inverse, scale=scale, dim=0).cpu().numpy().T)
+        assert np.array_equal(a.view(np.uint32), b.view(np.uint32)), (N, inverse)
+
+
 def test_fft_in_place_and_columns():
     rng = np.random.default_rng(7)
     x = crandn(rng, 4, 2048)
