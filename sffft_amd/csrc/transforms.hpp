@@ -207,9 +207,8 @@ __global__ void __launch_bounds__(128)
 // stages), so the results are bit-identical to the staged path. One LDS slot of padding
 // per 16 elements keeps the threads of the last stage (R consecutive elements each) on
 // different banks.
-constexpr int ONEPASS_MAX_N = 8192;
+constexpr int ONEPASS_MAX_N = 16384;  // 136 KB of LDS
 constexpr int ONEPASS_SLOTS = 4096;
-constexpr int ONEPASS_THREADS = 256;
 
 __device__ __forceinline__ int lpad(int p) { return p + (p >> 4); }
 
@@ -217,6 +216,8 @@ template <int N>
 struct LineGeom {
   static constexpr int G = N >= ONEPASS_SLOTS ? 1 : ONEPASS_SLOTS / N;  // sequences per workgroup
   static constexpr int SLOTS = G * N;
+  // one thread per radix-16 line: 256 threads, 512 at N = 8192, 1024 at N = 16384
+  static constexpr int THREADS = SLOTS / MAX_RADIX;
   static constexpr int LDS = SLOTS + SLOTS / 16;
   // radix of the stage whose remaining product of radices is REST (16s first)
   static constexpr int radix(int rest) { return rest > MAX_RADIX ? MAX_RADIX : rest; }
@@ -229,7 +230,7 @@ __device__ __forceinline__ void line_stage(float2* buf, const double* wc, const 
   constexpr int R = LineGeom<N>::radix(REST), sJ = REST / R, LPS = N / R;
   constexpr int LINES = LineGeom<N>::G * LPS;
   constexpr bool LAST = REST == R;
-  for (int li = threadIdx.x; li < LINES; li += ONEPASS_THREADS) {
+  for (int li = threadIdx.x; li < LINES; li += LineGeom<N>::THREADS) {
     const int g = li / LPS, l = li - g * LPS;
     const int inner = l % sJ, base = g * N + (l / sJ) * REST + inner;
     double vr[R], vi[R];
@@ -274,7 +275,7 @@ __device__ __forceinline__ int line_position(int f) {
 }
 
 template <int N>
-__global__ void __launch_bounds__(ONEPASS_THREADS)
+__global__ void __launch_bounds__(LineGeom<N>::THREADS)
     line_kernel(const float2* in, float2* out, Seqs q, int sign, float scale) {
   typedef LineGeom<N> LG;
   __shared__ float2 buf[LG::LDS];
@@ -287,13 +288,13 @@ __global__ void __launch_bounds__(ONEPASS_THREADS)
   }
   const long long s0 = (long long)blockIdx.x * LG::G;
   const int G = q.nseq - s0 < LG::G ? (int)(q.nseq - s0) : LG::G;
-  for (int i = threadIdx.x; i < LG::SLOTS; i += ONEPASS_THREADS) {
+  for (int i = threadIdx.x; i < LG::SLOTS; i += LG::THREADS) {
     const int g = i / N;
     buf[lpad(i)] = g < G ? in[q.base(s0 + g) + (i - g * N)] : make_float2(0.f, 0.f);
   }
   __syncthreads();
   line_stage<N, N>(buf, wc, ws, sign, scale);
-  for (int i = threadIdx.x; i < G * N; i += ONEPASS_THREADS) {
+  for (int i = threadIdx.x; i < G * N; i += LG::THREADS) {
     const int g = i / N, f = i - g * N;
     out[q.base(s0 + g) + f] = buf[lpad(g * N + line_position<N>(f))];
   }
@@ -302,7 +303,7 @@ __global__ void __launch_bounds__(ONEPASS_THREADS)
 template <int N>
 inline void launch_line(const float2* in, float2* out, const Seqs& q, int sign, float scale, hipStream_t st) {
   const unsigned grid = (unsigned)((q.nseq + LineGeom<N>::G - 1) / LineGeom<N>::G);
-  hipLaunchKernelGGL(line_kernel<N>, dim3(grid), dim3(ONEPASS_THREADS), 0, st, in, out, q, sign, scale);
+  hipLaunchKernelGGL(line_kernel<N>, dim3(grid), dim3(LineGeom<N>::THREADS), 0, st, in, out, q, sign, scale);
 }
 
 inline bool run_lines(const float2* in, float2* out, const Seqs& q, int N, int sign, float scale, hipStream_t st) {
@@ -321,6 +322,7 @@ inline bool run_lines(const float2* in, float2* out, const Seqs& q, int N, int s
     case 2048: launch_line<2048>(in, out, q, sign, scale, st); return true;
     case 4096: launch_line<4096>(in, out, q, sign, scale, st); return true;
     case 8192: launch_line<8192>(in, out, q, sign, scale, st); return true;
+    case 16384: launch_line<16384>(in, out, q, sign, scale, st); return true;
     default: return false;
   }
 }

@@ -60,9 +60,10 @@ def test_fft_closed_forms(N):
     assert np.abs(Xi[0] - ei).max() <= 2e-6 * N
 
 
-@pytest.mark.parametrize("batch,N", [(3, 2), (64, 16), (9, 256), (5, 1024), (4, 2048), (3, 4096), (3, 8192)])
+@pytest.mark.parametrize("batch,N", [(3, 2), (64, 16), (9, 256), (5, 1024), (4, 2048), (3, 4096), (3, 8192),
+                                     (2, 16384)])
 def test_one_pass_matches_staged_path_bitwise(batch, N):
-    """Contiguous sequences of N <= 8192 take the one-pass kernel (every stage in LDS); the
+    """Contiguous sequences of N <= 16384 take the one-pass kernel (every stage in LDS); the
     same values as the columns of a matrix take the staged kernels. The stages do the
     same arithmetic, so the two agree bit for bit, forward and inverse with a scale."""
     print(f"one-pass vs staged batch={batch} N={N}", flush=True)
