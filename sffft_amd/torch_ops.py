@@ -160,6 +160,7 @@ class LongConv:
     """
 
     def __init__(self, plan: Optional[Plan] = None):
+        self._plans: dict = {}  # (L, io, B) -> (plan, its fields)
         self.plan = plan
         # id(filter) -> (weak reference to it, (version, shape, plan), spectrum); an entry is
         # dropped when its filter is freed (tensors compare elementwise, so they cannot key a
@@ -167,11 +168,26 @@ class LongConv:
         self._cache: dict = {}
         self.spectra_computed = 0
 
+    @property
+    def plan(self) -> Optional[Plan]:
+        return self._plan
+
+    @plan.setter
+    def plan(self, plan: Optional[Plan]) -> None:
+        self._plan = plan
+        self._plans.clear()
+
     def plan_for(self, u: torch.Tensor) -> Plan:
-        if self.plan is not None:
-            return self.plan
+        return self._plan_and_fields(u)[0]
+
+    def _plan_and_fields(self, u: torch.Tensor):
         io = "bf16" if u.dtype == torch.bfloat16 else "fp32"
-        return default_plan(u.shape[-1], io, u.shape[0])
+        key = (u.shape[-1], io, u.shape[0])
+        hit = self._plans.get(key)
+        if hit is None:
+            plan = self.plan if self.plan is not None else default_plan(key[0], io, key[2])
+            hit = self._plans[key] = (plan, plan_fields(plan))
+        return hit
 
     def spectrum(self, k: torch.Tensor, plan: Plan) -> torch.Tensor:
         fields = plan_fields(plan)
@@ -190,9 +206,14 @@ class LongConv:
         return kf
 
     def __call__(self, u: torch.Tensor, k: torch.Tensor) -> torch.Tensor:
-        plan = self.plan_for(u)
-        fields = plan_fields(plan)
+        plan, fields = self._plan_and_fields(u)
         kf = self.spectrum(k, plan)
-        if k.requires_grad and torch.is_grad_enabled():
+        grad = torch.is_grad_enabled()
+        if grad and k.requires_grad:
             return _LongConvFn.apply(u, k, kf, fields)
-        return torch.ops.sffft.conv(u, kf, fields)
+        if (grad and u.requires_grad) or torch.compiler.is_compiling():
+            return torch.ops.sffft.conv(u, kf, fields)
+        # Nothing to differentiate and no graph being traced: the same kernel through the C
+        # ABI, without the operator's Python dispatch (about half the host time of a call,
+        # which at L <= 2048 is longer than the kernel).
+        return _conv(u, kf, plan)

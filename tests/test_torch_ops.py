@@ -212,6 +212,26 @@ def test_spectrum_cache(dev):
 
 
 @pytest.mark.gpu
+def test_longconv_without_gradients(dev):
+    """With nothing to differentiate LongConv calls the C ABI directly, skipping the operator's
+    dispatch; the outputs are the operator's, bit for bit."""
+    u, k, _, _ = _inputs(dev, 4, 5, 1024, seed=8)
+    lc = torch_ops.LongConv()
+    with torch.no_grad():
+        y_fast = lc(u, k)
+    y_plain = lc(u, k)  # grad enabled, but neither input requires it: also the direct call
+    p = torch_ops.plan_fields(lc.plan_for(u))
+    y_op = torch.ops.sffft.conv(u, torch.ops.sffft.spectrum(k, p), p)
+    ur = u.clone().requires_grad_()
+    y_grad = lc(ur, k)  # the operator, with its autograd
+    assert not y_fast.requires_grad and y_grad.requires_grad
+    assert torch.equal(y_fast, y_op) and torch.equal(y_plain, y_op) and torch.equal(y_grad.detach(), y_op)
+    # a plan set on the layer replaces the cached default
+    lc.plan = sf.make_plan("32x32", 4, seqs=2, mode=1, channels=1)
+    assert lc.plan_for(u.to(torch.bfloat16)).waves == 4 and lc.plan_for(u).r0 == 32
+
+
+@pytest.mark.gpu
 def test_torch_compile(dev):
     u, k, _, _ = _inputs(dev, 2, 6, 512, seed=6)
     p = torch_ops.plan_fields(sf.default_plan(512, "fp32", 2))
