@@ -1,13 +1,14 @@
 # Top-level targets of the reference's Makefile (Makefile:8-24 there): build, the CPU
 # tests, the GPU tests and one benchmark line. The build itself is sffft_amd/Makefile
 # (gfx950 kernels, the C-ABI library, the `sffft` driver, the rocFFT comparator and the
-# race-check build).
+# race-check build) and sffft_amd/torch.mk (the PyTorch operators).
 PYTHON ?= python3
 
 .PHONY: all sffft test test-gpu bench clean
 
 all:
 	$(MAKE) -C sffft_amd
+	$(MAKE) -C sffft_amd -f torch.mk
 
 # the `sffft` driver (the reference's default target)
 sffft:
@@ -29,3 +30,4 @@ bench: all
 
 clean:
 	$(MAKE) -C sffft_amd clean
+	$(MAKE) -C sffft_amd -f torch.mk clean

@@ -9,9 +9,12 @@ long-convolution layers of Hyena/H3/S4-style models (README.md:11). This module 
 - ``LongConv``: the two together, with the spectrum cached per (filter tensor, its version, L,
   plan), so a layer whose filter does not change computes the spectrum once.
 
-``plan`` is the list of the nine ``sffft_plan`` fields (``plan_fields``). Both operators have fake
-(meta) implementations, so they trace under ``torch.compile`` and ``torch.export``, and they are
-plain stream-ordered launches, so they capture into CUDA/HIP graphs.
+``plan`` is the list of the nine ``sffft_plan`` fields (``plan_fields``). The operators, their GPU
+kernels and their autograd are registered from C++ (``csrc/torch_ops.cpp``, built into
+``libsffft_torch.so``), so a call costs the dispatcher's few microseconds rather than the
+Python wrappers of ``torch.library.custom_op``. Their fake (meta) implementations are here, so
+they trace under ``torch.compile`` and ``torch.export``; they launch on the current stream, so
+they capture into CUDA/HIP graphs.
 
 Gradients:
 
@@ -26,14 +29,20 @@ Gradients:
 """
 from __future__ import annotations
 
+import os
 import weakref
-from typing import List, Optional, Sequence
+from typing import List, Optional
 
 import torch
 
-from . import LONG_DEFAULT_PLANS, Plan, conv as _conv, default_plan, spectrum as _spectrum
+from . import LONG_DEFAULT_PLANS, Plan, default_plan
 
 PLAN_FIELDS = ("r0", "r1", "r2", "waves", "acc", "cached", "seqs", "mode", "channels")
+
+OPS_LIB = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libsffft_torch.so")
+if not os.path.exists(OPS_LIB):
+    raise RuntimeError(f"{OPS_LIB} is missing: build it with `make -C sffft_amd` (or __graft_entry__.build())")
+torch.ops.load_library(OPS_LIB)  # defines sffft::spectrum and sffft::conv
 
 
 def plan_fields(plan: Plan) -> List[int]:
@@ -41,67 +50,20 @@ def plan_fields(plan: Plan) -> List[int]:
     return [int(getattr(plan, f)) for f in PLAN_FIELDS]
 
 
-def _plan(fields: Sequence[int]) -> Plan:
-    if len(fields) != len(PLAN_FIELDS):
-        raise ValueError(f"a plan has {len(PLAN_FIELDS)} fields {PLAN_FIELDS}, got {len(fields)}")
-    return Plan(*[int(x) for x in fields])
-
-
-@torch.library.custom_op("sffft::spectrum", mutates_args=(), device_types="cuda")
-def spectrum(k: torch.Tensor, plan: List[int]) -> torch.Tensor:
-    """Kernel-order spectrum of the real filters k [H, L] fp32 for the given plan."""
-    return _spectrum(k, k.shape[1], _plan(plan))
-
-
-@spectrum.register_fake
+@torch.library.register_fake("sffft::spectrum")
 def _spectrum_fake(k, plan):
     torch._check(k.dim() == 2, lambda: "k must be [H, L]")
     torch._check(k.dtype == torch.float32, lambda: "k must be float32")
     return k.new_empty((k.shape[0], 2 * k.shape[1]), dtype=torch.complex64)
 
 
-def _no_filter_grad(ctx, grad):
-    raise RuntimeError("sffft::spectrum has no gradient with respect to the filter")
-
-
-def _spectrum_setup(ctx, inputs, output):
-    pass
-
-
-spectrum.register_autograd(_no_filter_grad, setup_context=_spectrum_setup)
-
-
-@torch.library.custom_op("sffft::conv", mutates_args=(), device_types="cuda")
-def conv(u: torch.Tensor, kf: torch.Tensor, plan: List[int]) -> torch.Tensor:
-    """y[b, h, n] = sum_{m <= n} u[b, h, m] k[h, n - m] for u [B, H, L] fp32 or bf16 and kf
-    from ``spectrum`` with the same plan."""
-    return _conv(u, kf, _plan(plan))
-
-
-@conv.register_fake
+@torch.library.register_fake("sffft::conv")
 def _conv_fake(u, kf, plan):
     torch._check(u.dim() == 3, lambda: "u must be [B, H, L]")
     torch._check(u.dtype in (torch.float32, torch.bfloat16), lambda: "u must be float32 or bfloat16")
     torch._check(kf.dim() == 2 and kf.shape[0] == u.shape[1] and kf.shape[1] == 2 * u.shape[2],
                  lambda: "kf must be [H, 2L]")
     return torch.empty_like(u)
-
-
-def _conv_setup(ctx, inputs, output):
-    _, kf, plan = inputs
-    ctx.save_for_backward(kf)
-    ctx.plan = list(plan)
-
-
-def _conv_backward(ctx, dy):
-    (kf,) = ctx.saved_tensors
-    du = None
-    if ctx.needs_input_grad[0]:
-        du = torch.ops.sffft.conv(dy.flip(-1).contiguous(), kf, ctx.plan).flip(-1)
-    return du, None, None
-
-
-conv.register_autograd(_conv_backward, setup_context=_conv_setup)
 
 
 def filter_grad(u: torch.Tensor, dy: torch.Tensor) -> torch.Tensor:
@@ -208,12 +170,6 @@ class LongConv:
     def __call__(self, u: torch.Tensor, k: torch.Tensor) -> torch.Tensor:
         plan, fields = self._plan_and_fields(u)
         kf = self.spectrum(k, plan)
-        grad = torch.is_grad_enabled()
-        if grad and k.requires_grad:
+        if k.requires_grad and torch.is_grad_enabled():
             return _LongConvFn.apply(u, k, kf, fields)
-        if (grad and u.requires_grad) or torch.compiler.is_compiling():
-            return torch.ops.sffft.conv(u, kf, fields)
-        # Nothing to differentiate and no graph being traced: the same kernel through the C
-        # ABI, without the operator's Python dispatch (about half the host time of a call,
-        # which at L <= 2048 is longer than the kernel).
-        return _conv(u, kf, plan)
+        return torch.ops.sffft.conv(u, kf, fields)
