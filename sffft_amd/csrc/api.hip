@@ -426,6 +426,16 @@ __global__ void zero_fill_kernel(float2* __restrict__ p, size_t n) {
   if (i < n) p[i] = make_float2(0.f, 0.f);
 }
 
+// Filter rows k[h][0..klen) as complex rows of length N, zero-padded (the spectrum's input).
+__global__ void spectrum_pad_kernel(const float* __restrict__ k, float2* __restrict__ w, int klen, int N,
+                                    size_t n) {
+  const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  const size_t h = i / (size_t)N;
+  const int p = (int)(i - h * (size_t)N);
+  w[i] = make_float2(p < klen ? k[h * (size_t)klen + p] : 0.f, 0.f);
+}
+
 __global__ void to_bf16_kernel(const float* __restrict__ x, uint16_t* __restrict__ y, size_t n) {
   const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i < n) y[i] = f32_to_bf16(x[i]);
@@ -568,6 +578,20 @@ int spectrum_impl(const float* k, int H, int L, int klen, const sffft_plan* plan
   hipStream_t s = (hipStream_t)stream;
   float2* w = static_cast<float2*>(work);
   const float* kh = k + (size_t)h0 * klen;
+  if (N <= xf::ONEPASS_MAX_N) {
+    // The padded rows, their forward DFT in place (the one-pass transform: fp64 stages,
+    // complex64 between them, no workspace), then natural order -> kernel order.
+    const size_t n = (size_t)H * N;
+    hipLaunchKernelGGL(spectrum_pad_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, kh, w, klen, N, n);
+    int st = hip_status(hipGetLastError(), "spectrum pad launch");
+    if (st) return st;
+    const xf::Seqs q{H, 1, 0, N, 1, 0};
+    if ((st = hip_status(xf::run(w, w, nullptr, q, N, 0, 1.f, s), "spectrum transform launch"))) return st;
+    return permute_launch(w, static_cast<float2*>(kf), H, plan, 1, imag, whole, s, h0, Htot);
+  }
+  // Longer rows: one dense fp64 DFT stage per digit of the plan, then digit order -> kernel
+  // order (the one-pass transform stops at 16384 points, and `work` leaves no room for the
+  // staged transform's own workspace).
   for (int J = 0; J < S; J++) {
     const int R = J == 0 ? plan->r0 : J == 1 ? plan->r1 : plan->r2;
     const size_t threads = (size_t)H * (N / R);

@@ -76,6 +76,24 @@ def test_one_pass_matches_staged_path_bitwise(batch, N):
         assert np.array_equal(a.view(np.uint32), b.view(np.uint32)), (N, inverse)
 
 
+@pytest.mark.parametrize("L", [128, 1024, 8192, 16384])
+def test_spectrum_matches_fp64_dft(L):
+    """sffft_spectrum against the same kernel-order gather (sffft_spectrum_from_natural)
+    applied to numpy's fp64 DFT of the zero-padded filters, rounded to complex64, for every
+    compiled plan. Up to N = 16384 the spectrum runs the one-pass transform above; at
+    L = 16384 (N = 32768) one dense fp64 DFT stage per digit of the plan."""
+    print(f"spectrum L={L}", flush=True)
+    H = 7
+    k = np.random.default_rng(L + 1).standard_normal((H, L)).astype(np.float32)
+    nat = np.fft.fft(np.pad(k.astype(np.float64), ((0, 0), (0, L))), axis=1).astype(np.complex64)
+    kd = torch.from_numpy(k).to(DEV)
+    nat_d = torch.from_numpy(nat).to(DEV)
+    for plan in sf.plans(L):
+        got = sf.spectrum(kd, L, plan).cpu().numpy()
+        ref = sf.spectrum_from_natural(nat_d, L, plan).cpu().numpy()
+        assert rel(got, ref) <= 1e-6, (L, plan, rel(got, ref))
+
+
 def test_fft_in_place_and_columns():
     rng = np.random.default_rng(7)
     x = crandn(rng, 4, 2048)
