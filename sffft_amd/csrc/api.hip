@@ -578,20 +578,26 @@ int spectrum_impl(const float* k, int H, int L, int klen, const sffft_plan* plan
   hipStream_t s = (hipStream_t)stream;
   float2* w = static_cast<float2*>(work);
   const float* kh = k + (size_t)h0 * klen;
-  if (N <= xf::ONEPASS_MAX_N) {
-    // The padded rows, their forward DFT in place (the one-pass transform: fp64 stages,
-    // complex64 between them, no workspace), then natural order -> kernel order.
+  // The padded rows, their forward DFT in place in `work` (fp64 stages, complex64 between
+  // them), then natural order -> kernel order. Up to 16384 points the transform is one pass
+  // through LDS and needs no workspace. Longer rows (kernel-order spectra of H * N values,
+  // modes 0 and 2) take the staged transform, whose workspace is this call's own rows of kf:
+  // the gather overwrites them afterwards, and no earlier result lives there. An imaginary
+  // part (imag) is added onto kf's real part's result, so it cannot lend kf; it takes the
+  // dense stages below.
+  const bool onepass = N <= xf::ONEPASS_MAX_N;
+  if (onepass || (!imag && plan->mode != 1)) {
     const size_t n = (size_t)H * N;
     hipLaunchKernelGGL(spectrum_pad_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, kh, w, klen, N, n);
     int st = hip_status(hipGetLastError(), "spectrum pad launch");
     if (st) return st;
     const xf::Seqs q{H, 1, 0, N, 1, 0};
-    if ((st = hip_status(xf::run(w, w, nullptr, q, N, 0, 1.f, s), "spectrum transform launch"))) return st;
+    float2* scratch = onepass ? nullptr : static_cast<float2*>(kf) + (size_t)h0 * N;
+    if ((st = hip_status(xf::run(w, w, scratch, q, N, 0, 1.f, s), "spectrum transform launch"))) return st;
     return permute_launch(w, static_cast<float2*>(kf), H, plan, 1, imag, whole, s, h0, Htot);
   }
-  // Longer rows: one dense fp64 DFT stage per digit of the plan, then digit order -> kernel
-  // order (the one-pass transform stops at 16384 points, and `work` leaves no room for the
-  // staged transform's own workspace).
+  // The imaginary part of a complex filter's spectrum beyond 16384 points: one dense fp64 DFT
+  // stage per digit of the plan, then digit order -> kernel order.
   for (int J = 0; J < S; J++) {
     const int R = J == 0 ? plan->r0 : J == 1 ? plan->r1 : plan->r2;
     const size_t threads = (size_t)H * (N / R);

@@ -76,12 +76,13 @@ def test_one_pass_matches_staged_path_bitwise(batch, N):
         assert np.array_equal(a.view(np.uint32), b.view(np.uint32)), (N, inverse)
 
 
-@pytest.mark.parametrize("L", [128, 1024, 8192, 16384])
+@pytest.mark.parametrize("L", [128, 1024, 8192, 16384, 32768])
 def test_spectrum_matches_fp64_dft(L):
     """sffft_spectrum against the same kernel-order gather (sffft_spectrum_from_natural)
     applied to numpy's fp64 DFT of the zero-padded filters, rounded to complex64, for every
-    compiled plan. Up to N = 16384 the spectrum runs the one-pass transform above; at
-    L = 16384 (N = 32768) one dense fp64 DFT stage per digit of the plan."""
+    compiled plan. Up to N = 16384 the spectrum runs the one-pass transform above, beyond it
+    the staged transform with the spectrum's own rows as workspace (L = 16384: workgroup
+    plans; L = 32768: multi-pass plans)."""
     print(f"spectrum L={L}", flush=True)
     H = 7
     k = np.random.default_rng(L + 1).standard_normal((H, L)).astype(np.float32)
