@@ -308,65 +308,10 @@ __device__ inline void kernel_order_digits_rt(int idx, int r0, int r1, int r2, i
   }
 }
 
-// One in-place decimation-in-frequency stage over digit J (Appendix-A order of the
-// reference: after all stages position p = d0*(R1 R2) + d1*R2 + d2 holds
-// DFT_N(pad(k))[d0 + R0 d1 + R0 R1 d2]). One thread per line of R_J points; fp64
-// arithmetic, fp32 storage. Stage 0 reads the real filter rows of length klen (L, or N for
-// a circular convolution), zero-padded to N.
-__global__ void spectrum_stage_kernel(const float* __restrict__ k, float2* work, int H, int klen, int r0, int r1,
-                                      int r2, int J) {
-  __shared__ double wc[64], ws[64];
-  const int N = r0 * r1 * r2, S = r2 > 1 ? 3 : 2;
-  const int R = J == 0 ? r0 : J == 1 ? r1 : r2;
-  const int sJ = J == 0 ? r1 * r2 : J == 1 ? r2 : 1;
-  for (int i = threadIdx.x; i < R; i += blockDim.x) {
-    double s, c;
-    sincospi(2.0 * (double)i / (double)R, &s, &c);
-    wc[i] = c;
-    ws[i] = s;
-  }
-  __syncthreads();
-  const int lines = N / R;
-  const size_t gid = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (gid >= (size_t)H * lines) return;
-  const int h = (int)(gid / lines), l = (int)(gid % lines);
-  const int inner = l % sJ, outer = l / sJ;
-  const int base = outer * R * sJ + inner;
-  float2* row = work + (size_t)h * N;
-  float2 x[64];
-  for (int t = 0; t < R; t++) {
-    const int p = base + t * sJ;
-    if (J == 0)
-      x[t] = make_float2(p < klen ? k[(size_t)h * klen + p] : 0.f, 0.f);
-    else
-      x[t] = row[p];
-  }
-  const int mul = N / (R * sJ);
-  for (int kk = 0; kk < R; kk++) {
-    double ar = 0.0, ai = 0.0;
-    for (int t = 0; t < R; t++) {
-      const int e = (t * kk) % R;
-      const double c = wc[e], s = ws[e];  // exp(-i theta) = c - i s
-      ar += (double)x[t].x * c + (double)x[t].y * s;
-      ai += (double)x[t].y * c - (double)x[t].x * s;
-    }
-    if (J != S - 1) {
-      const int e = (mul * inner * kk) % N;
-      double s, c;
-      sincospi(2.0 * (double)e / (double)N, &s, &c);
-      const double tr = ar * c + ai * s, ti = ai * c - ar * s;
-      ar = tr;
-      ai = ti;
-    }
-    row[base + kk * sJ] = make_float2((float)ar, (float)ai);
-  }
-}
-
-// Gather into the fused kernel's order, folding in 1/sqrt(R_last) of the last
-// forward stage. src is p-order (natural == 0) or natural frequency order. With imag,
-// the gathered values are the spectrum of a filter's imaginary part: kf += i * value.
+// Gather of a natural-order spectrum into the fused kernel's order, folding in
+// 1/sqrt(R_last) of the last forward stage.
 __global__ void spectrum_permute_kernel(const float2* __restrict__ src, float2* __restrict__ kf, int H, int r0,
-                                        int r1, int r2, int mode, int natural, float scale, int imag = 0) {
+                                        int r1, int r2, int mode, float scale) {
   const int N = r0 * r1 * r2;
   const size_t gid = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (gid >= (size_t)H * N) return;
@@ -377,18 +322,13 @@ __global__ void spectrum_permute_kernel(const float2* __restrict__ src, float2* 
     // pipeline's sp_index over the row plan r1 x r2) of frequencies k1 + r0*(k0' + r1*k1')
     const int NR = r1 * r2, row = idx / NR;
     kernel_order_digits_rt(idx - row * NR, r1, r2, 1, 1, k0, k1, k2);
-    s = natural ? row + r0 * (k0 + r1 * k1) : row * NR + k0 * r2 + k1;
+    s = row + r0 * (k0 + r1 * k1);
   } else {
     kernel_order_digits_rt(idx, r0, r1, r2, mode, k0, k1, k2);
-    s = natural ? k0 + r0 * k1 + r0 * r1 * k2 : k0 * (r1 * r2) + k1 * r2 + k2;
+    s = k0 + r0 * k1 + r0 * r1 * k2;
   }
   const float2 v = src[(size_t)h * N + s];
-  if (imag) {
-    const float2 a = kf[gid];
-    kf[gid] = make_float2(a.x - v.y * scale, a.y + v.x * scale);
-  } else {
-    kf[gid] = make_float2(v.x * scale, v.y * scale);
-  }
+  kf[gid] = make_float2(v.x * scale, v.y * scale);
 }
 
 // Hermitian half of a real filter's spectrum in the wave pipeline's order
@@ -399,7 +339,7 @@ __global__ void spectrum_permute_kernel(const float2* __restrict__ src, float2* 
 // from channel h0 on; channels are consecutive in kf (C = 2*(r0/2 + 1)*PITCH complex
 // values each).
 __global__ void spectrum_half_kernel(const float2* __restrict__ src, float2* __restrict__ kf, int H, int h0, int r0,
-                                     int r1, int natural, float scale) {
+                                     int r1, float scale) {
   const int pitch = 8 * (r1 / 16) + 1, C = 2 * (r0 / 2 + 1) * pitch, N = r0 * r1;
   const size_t gid = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (gid >= (size_t)H * C) return;
@@ -414,7 +354,7 @@ __global__ void spectrum_half_kernel(const float2* __restrict__ src, float2* __r
   const int k1 = 16 * kt + 4 * g + 2 * q + e;
   const bool mid = k0 == r0 / 2;
   const int kk1 = mid ? r1 - 1 - k1 : k1;
-  const int sidx = natural ? k0 + r0 * kk1 : k0 * r1 + kk1;
+  const int sidx = k0 + r0 * kk1;
   const float2 v = src[(size_t)h * N + sidx];
   *out = make_float2(v.x * scale, (mid ? -v.y : v.y) * scale);
 }
@@ -426,14 +366,16 @@ __global__ void zero_fill_kernel(float2* __restrict__ p, size_t n) {
   if (i < n) p[i] = make_float2(0.f, 0.f);
 }
 
-// Filter rows k[h][0..klen) as complex rows of length N, zero-padded (the spectrum's input).
-__global__ void spectrum_pad_kernel(const float* __restrict__ k, float2* __restrict__ w, int klen, int N,
-                                    size_t n) {
+// Filter rows kr[h][0..klen) (+ i ki[h][..] for a complex filter, ki may be null) as complex
+// rows of length N, zero-padded: the spectrum's input.
+__global__ void spectrum_pad_kernel(const float* __restrict__ kr, const float* __restrict__ ki,
+                                    float2* __restrict__ w, int klen, int N, size_t n) {
   const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= n) return;
   const size_t h = i / (size_t)N;
   const int p = (int)(i - h * (size_t)N);
-  w[i] = make_float2(p < klen ? k[h * (size_t)klen + p] : 0.f, 0.f);
+  const size_t j = h * (size_t)klen + p;
+  w[i] = p < klen ? make_float2(kr[j], ki ? ki[j] : 0.f) : make_float2(0.f, 0.f);
 }
 
 __global__ void to_bf16_kernel(const float* __restrict__ x, uint16_t* __restrict__ y, size_t n) {
@@ -539,20 +481,18 @@ int long_plans_for(int L, const LongEntry** out, int cap) {
   return k;
 }
 
-// imag: k is the imaginary part of a complex filter; its spectrum is added times i to kf
-// Launches the gather of a p-order (natural = 0) or natural-order spectrum src of the H
-// channels from channel h0 on into the kernel order of the plan: the Hermitian half for
-// wave plans (mode 1) unless `whole` (complex filters), else the whole spectrum. kf is
-// the spectrum of all Htot channels; the gather of the last channels also zeroes what a
-// Hermitian half leaves unused.
-int permute_launch(const float2* src, float2* kf, int H, const sffft_plan* plan, int natural, int imag, int whole,
-                   hipStream_t s, int h0 = 0, int Htot = -1) {
+// Launches the gather of a natural-order spectrum src of the H channels from channel h0 on
+// into the kernel order of the plan: the Hermitian half for wave plans (mode 1) unless
+// `whole` (complex filters), else the whole spectrum. kf is the spectrum of all Htot
+// channels; the gather of the last channels also zeroes what a Hermitian half leaves unused.
+int permute_launch(const float2* src, float2* kf, int H, const sffft_plan* plan, int whole, hipStream_t s,
+                   int h0 = 0, int Htot = -1) {
   if (Htot < 0) Htot = H;
   const size_t N = (size_t)plan->r0 * plan->r1 * plan->r2;
   if (plan->mode == 1 && !whole) {
     const size_t C = (size_t)2 * (plan->r0 / 2 + 1) * (8 * (plan->r1 / 16) + 1), total = (size_t)H * C;
     hipLaunchKernelGGL(spectrum_half_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, src, kf, H, h0,
-                       plan->r0, plan->r1, natural, last_stage_scale(plan));
+                       plan->r0, plan->r1, last_stage_scale(plan));
     if (h0 + H == Htot) {
       const size_t tail = (size_t)Htot * (N - C);
       hipLaunchKernelGGL(zero_fill_kernel, dim3((unsigned)((tail + 255) / 256)), dim3(256), 0, s,
@@ -561,52 +501,35 @@ int permute_launch(const float2* src, float2* kf, int H, const sffft_plan* plan,
   } else {
     const size_t total = (size_t)H * N;
     hipLaunchKernelGGL(spectrum_permute_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, src,
-                       kf + (size_t)h0 * N, H, plan->r0, plan->r1, plan->r2, plan->mode, natural,
-                       last_stage_scale(plan), imag);
+                       kf + (size_t)h0 * N, H, plan->r0, plan->r1, plan->r2, plan->mode, last_stage_scale(plan));
   }
   return hip_status(hipGetLastError(), "spectrum permute launch");
 }
 
-// Spectrum of the H filter rows from channel h0 on (all Htot of them when Htot < 0),
-// staged through `work` (H * N complex64).
-int spectrum_impl(const float* k, int H, int L, int klen, const sffft_plan* plan, void* kf, void* work,
-                  void* stream, int imag = 0, int whole = 0, int h0 = 0, int Htot = -1) {
-  if (!k || !kf || !work || H < 1 || kf == work) return SFFFT_EINVAL;
+// Spectrum of the H filter rows from channel h0 on (all Htot of them when Htot < 0): kr, plus
+// i ki for a complex filter (ki non-null, whole spectrum). The padded rows are transformed
+// in place in `work` (H * N complex64; fp64 stages, complex64 between them), then gathered
+// into kernel order. Up to 16384 points the transform is one pass through LDS and needs no
+// workspace. Longer rows take the staged transform, whose workspace is this call's own rows
+// of kf: the gather overwrites them afterwards, and the results of earlier calls (channels
+// before h0, at most h0 * N values even as Hermitian halves) lie before them.
+int spectrum_impl(const float* kr, const float* ki, int H, int L, int klen, const sffft_plan* plan, void* kf,
+                  void* work, void* stream, int whole = 0, int h0 = 0, int Htot = -1) {
+  if (!kr || !kf || !work || H < 1 || kf == work) return SFFFT_EINVAL;
   const int rc = check_shape(L, plan);
   if (rc) return rc;
-  const int N = 2 * L, S = plan->r2 > 1 ? 3 : 2;
+  const int N = 2 * L;
   hipStream_t s = (hipStream_t)stream;
   float2* w = static_cast<float2*>(work);
-  const float* kh = k + (size_t)h0 * klen;
-  // The padded rows, their forward DFT in place in `work` (fp64 stages, complex64 between
-  // them), then natural order -> kernel order. Up to 16384 points the transform is one pass
-  // through LDS and needs no workspace. Longer rows (kernel-order spectra of H * N values,
-  // modes 0 and 2) take the staged transform, whose workspace is this call's own rows of kf:
-  // the gather overwrites them afterwards, and no earlier result lives there. An imaginary
-  // part (imag) is added onto kf's real part's result, so it cannot lend kf; it takes the
-  // dense stages below.
-  const bool onepass = N <= xf::ONEPASS_MAX_N;
-  if (onepass || (!imag && plan->mode != 1)) {
-    const size_t n = (size_t)H * N;
-    hipLaunchKernelGGL(spectrum_pad_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, kh, w, klen, N, n);
-    int st = hip_status(hipGetLastError(), "spectrum pad launch");
-    if (st) return st;
-    const xf::Seqs q{H, 1, 0, N, 1, 0};
-    float2* scratch = onepass ? nullptr : static_cast<float2*>(kf) + (size_t)h0 * N;
-    if ((st = hip_status(xf::run(w, w, scratch, q, N, 0, 1.f, s), "spectrum transform launch"))) return st;
-    return permute_launch(w, static_cast<float2*>(kf), H, plan, 1, imag, whole, s, h0, Htot);
-  }
-  // The imaginary part of a complex filter's spectrum beyond 16384 points: one dense fp64 DFT
-  // stage per digit of the plan, then digit order -> kernel order.
-  for (int J = 0; J < S; J++) {
-    const int R = J == 0 ? plan->r0 : J == 1 ? plan->r1 : plan->r2;
-    const size_t threads = (size_t)H * (N / R);
-    hipLaunchKernelGGL(spectrum_stage_kernel, dim3((unsigned)((threads + 127) / 128)), dim3(128), 0, s, kh, w, H,
-                       klen, plan->r0, plan->r1, plan->r2, J);
-    const int st = hip_status(hipGetLastError(), "spectrum stage launch");
-    if (st) return st;
-  }
-  return permute_launch(w, static_cast<float2*>(kf), H, plan, 0, imag, whole, s, h0, Htot);
+  const size_t off = (size_t)h0 * klen, n = (size_t)H * N;
+  hipLaunchKernelGGL(spectrum_pad_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, kr + off,
+                     ki ? ki + off : nullptr, w, klen, N, n);
+  int st = hip_status(hipGetLastError(), "spectrum pad launch");
+  if (st) return st;
+  const xf::Seqs q{H, 1, 0, N, 1, 0};
+  float2* scratch = N <= xf::ONEPASS_MAX_N ? nullptr : static_cast<float2*>(kf) + (size_t)h0 * N;
+  if ((st = hip_status(xf::run(w, w, scratch, q, N, 0, 1.f, s), "spectrum transform launch"))) return st;
+  return permute_launch(w, static_cast<float2*>(kf), H, plan, whole, s, h0, Htot);
 }
 }  // namespace
 }  // namespace sffft
@@ -687,7 +610,7 @@ size_t sffft_spectrum_bytes(int H, int L) {
 }
 
 int sffft_spectrum(const float* k, int H, int L, const sffft_plan* plan, void* kf, void* work, void* stream) {
-  return spectrum_impl(k, H, L, L, plan, kf, work, stream);
+  return spectrum_impl(k, nullptr, H, L, L, plan, kf, work, stream);
 }
 
 int sffft_spectrum_noalloc(const float* k, int H, int L, const sffft_plan* plan, void* kf, void* stream) {
@@ -704,7 +627,7 @@ int sffft_spectrum_noalloc(const float* k, int H, int L, const sffft_plan* plan,
   if ((rc = scratch_for_device(&work))) return rc;
   const int chunk = (int)std::min<size_t>((size_t)H, SFFFT_SCRATCH_BYTES / per);
   for (int h0 = 0; h0 < H; h0 += chunk)
-    if ((rc = spectrum_impl(k, std::min(chunk, H - h0), L, L, plan, kf, work, stream, 0, 0, h0, H))) return rc;
+    if ((rc = spectrum_impl(k, nullptr, std::min(chunk, H - h0), L, L, plan, kf, work, stream, 0, h0, H))) return rc;
   return SFFFT_OK;
 }
 
@@ -712,14 +635,13 @@ int sffft_spectrum_complex(const float* kr, const float* ki, int H, int L, const
                            void* work, void* stream) {
   // pairs of sequences per transform only: they carry the real and imaginary planes of u and y
   if (!plan || plan->seqs != 2 || !ki || ki == kr) return SFFFT_EINVAL;
-  const int rc = spectrum_impl(kr, H, L, L, plan, kf, work, stream, 0, 1);
-  return rc ? rc : spectrum_impl(ki, H, L, L, plan, kf, work, stream, 1, 1);
+  return spectrum_impl(kr, ki, H, L, L, plan, kf, work, stream, 1);
 }
 
 int sffft_spectrum_circular(const float* k, int H, int N, const sffft_plan* plan, void* kf, void* work,
                             void* stream) {
   if (N < 2 || N % 2 || !plan || plan->mode != 2) return SFFFT_EINVAL;
-  return spectrum_impl(k, H, N / 2, N, plan, kf, work, stream);
+  return spectrum_impl(k, nullptr, H, N / 2, N, plan, kf, work, stream);
 }
 
 int sffft_circconv_long_f32(const float* u, const void* kf, float* y, void* work, size_t work_bytes, int B, int H,
@@ -738,8 +660,7 @@ int sffft_spectrum_from_natural(const void* kc, int H, int L, const sffft_plan* 
   if (!kc || !kf || H < 1 || kc == kf) return SFFFT_EINVAL;
   const int rc = check_shape(L, plan);
   if (rc) return rc;
-  return permute_launch(static_cast<const float2*>(kc), static_cast<float2*>(kf), H, plan, 1, 0, 0,
-                        (hipStream_t)stream);
+  return permute_launch(static_cast<const float2*>(kc), static_cast<float2*>(kf), H, plan, 0, (hipStream_t)stream);
 }
 
 int sffft_conv_f32(const float* u, const void* kf, float* y, int B, int H, int L, const sffft_plan* plan,
