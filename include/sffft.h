@@ -95,6 +95,12 @@ size_t sffft_spectrum_bytes(int H, int L);
  * Arithmetic: fp64 accumulation and twiddles, fp32 storage between the stages. */
 int sffft_spectrum(const float* k, int H, int L, const sffft_plan* plan, void* kf, void* work, void* stream);
 
+/* sffft_spectrum of the conjugate spectrum conj(K), same layout and arguments. No counterpart
+ * in the reference: it serves the gradients of the convolution. With the 2L zero padding the
+ * anti-causal correlation z[m] = sum_{n>=m} x[n] k[n-m] (m < L), which the input and filter
+ * gradients are, is sffft_conv_* of x with this spectrum: no time reversal of x or z. */
+int sffft_spectrum_conj(const float* k, int H, int L, const sffft_plan* plan, void* kf, void* work, void* stream);
+
 /* sffft_spectrum without the `work` argument, for callers that cannot allocate (code under
  * HIP graph capture, serving loops, harnesses that forbid hipMalloc). No counterpart in the
  * reference. It stages the channels through a static device array of 32 MiB per GPU (held

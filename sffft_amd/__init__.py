@@ -109,6 +109,7 @@ def load_library(path: str) -> ctypes.CDLL:
         "sffft_plan_get": (ci, [ci, ci, P, ctypes.c_char_p, sz]),
         "sffft_spectrum_bytes": (sz, [ci, ci]),
         "sffft_spectrum": (ci, [vp, ci, ci, P, vp, vp, vp]),
+        "sffft_spectrum_conj": (ci, [vp, ci, ci, P, vp, vp, vp]),
         "sffft_spectrum_from_natural": (ci, [vp, ci, ci, P, vp, vp]),
         "sffft_spectrum_noalloc": (ci, [vp, ci, ci, P, vp, vp]),
         "sffft_conv_f32": (ci, [vp, vp, vp, ci, ci, ci, P, vp]),
@@ -261,8 +262,10 @@ def _ptr(t) -> ctypes.c_void_p:
     return ctypes.c_void_p(t.data_ptr())
 
 
-def spectrum(k, L: int, plan: Plan, work=None):
-    """Kernel-order filter spectrum [H, 2L] complex64 from the real filter k [H, L] (fp32, cuda)."""
+def spectrum(k, L: int, plan: Plan, work=None, conj: bool = False):
+    """Kernel-order filter spectrum [H, 2L] complex64 from the real filter k [H, L] (fp32, cuda);
+    with conj, the conjugate spectrum (sffft_spectrum_conj), on which sffft_conv_* computes the
+    anti-causal correlation sum_{n>=m} x[n] k[n-m] instead of the causal convolution."""
     import torch
 
     assert k.is_cuda and k.dtype == torch.float32 and k.dim() == 2 and k.shape[1] == L
@@ -271,8 +274,8 @@ def spectrum(k, L: int, plan: Plan, work=None):
     kf = torch.empty((H, 2 * L), dtype=torch.complex64, device=k.device)
     if work is None:
         work = torch.empty_like(kf)
-    _check(lib().sffft_spectrum(_ptr(k), H, L, ctypes.byref(plan), _ptr(kf), _ptr(work), _stream()),
-           "sffft_spectrum")
+    fn = lib().sffft_spectrum_conj if conj else lib().sffft_spectrum
+    _check(fn(_ptr(k), H, L, ctypes.byref(plan), _ptr(kf), _ptr(work), _stream()), "sffft_spectrum")
     return kf
 
 

@@ -309,9 +309,10 @@ __device__ inline void kernel_order_digits_rt(int idx, int r0, int r1, int r2, i
 }
 
 // Gather of a natural-order spectrum into the fused kernel's order, folding in
-// 1/sqrt(R_last) of the last forward stage.
+// 1/sqrt(R_last) of the last forward stage: real parts times scale, imaginary parts times
+// iscale (-scale gathers the conjugate spectrum).
 __global__ void spectrum_permute_kernel(const float2* __restrict__ src, float2* __restrict__ kf, int H, int r0,
-                                        int r1, int r2, int mode, float scale) {
+                                        int r1, int r2, int mode, float scale, float iscale) {
   const int N = r0 * r1 * r2;
   const size_t gid = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (gid >= (size_t)H * N) return;
@@ -328,7 +329,7 @@ __global__ void spectrum_permute_kernel(const float2* __restrict__ src, float2* 
     s = k0 + r0 * k1 + r0 * r1 * k2;
   }
   const float2 v = src[(size_t)h * N + s];
-  kf[gid] = make_float2(v.x * scale, v.y * scale);
+  kf[gid] = make_float2(v.x * scale, v.y * iscale);
 }
 
 // Hermitian half of a real filter's spectrum in the wave pipeline's order
@@ -339,7 +340,7 @@ __global__ void spectrum_permute_kernel(const float2* __restrict__ src, float2* 
 // from channel h0 on; channels are consecutive in kf (C = 2*(r0/2 + 1)*PITCH complex
 // values each).
 __global__ void spectrum_half_kernel(const float2* __restrict__ src, float2* __restrict__ kf, int H, int h0, int r0,
-                                     int r1, float scale) {
+                                     int r1, float scale, float iscale) {
   const int pitch = 8 * (r1 / 16) + 1, C = 2 * (r0 / 2 + 1) * pitch, N = r0 * r1;
   const size_t gid = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (gid >= (size_t)H * C) return;
@@ -356,7 +357,7 @@ __global__ void spectrum_half_kernel(const float2* __restrict__ src, float2* __r
   const int kk1 = mid ? r1 - 1 - k1 : k1;
   const int sidx = k0 + r0 * kk1;
   const float2 v = src[(size_t)h * N + sidx];
-  *out = make_float2(v.x * scale, (mid ? -v.y : v.y) * scale);
+  *out = make_float2(v.x * scale, (mid ? -v.y : v.y) * iscale);
 }
 
 // Zeroes n complex values (the part of a spectrum buffer a Hermitian half leaves unused,
@@ -483,16 +484,18 @@ int long_plans_for(int L, const LongEntry** out, int cap) {
 
 // Launches the gather of a natural-order spectrum src of the H channels from channel h0 on
 // into the kernel order of the plan: the Hermitian half for wave plans (mode 1) unless
-// `whole` (complex filters), else the whole spectrum. kf is the spectrum of all Htot
-// channels; the gather of the last channels also zeroes what a Hermitian half leaves unused.
-int permute_launch(const float2* src, float2* kf, int H, const sffft_plan* plan, int whole, hipStream_t s,
+// `whole` (complex filters), else the whole spectrum; with conj, of the conjugate spectrum.
+// kf is the spectrum of all Htot channels; the gather of the last channels also zeroes what
+// a Hermitian half leaves unused.
+int permute_launch(const float2* src, float2* kf, int H, const sffft_plan* plan, int whole, int conj, hipStream_t s,
                    int h0 = 0, int Htot = -1) {
+  const float sc = last_stage_scale(plan), isc = conj ? -sc : sc;
   if (Htot < 0) Htot = H;
   const size_t N = (size_t)plan->r0 * plan->r1 * plan->r2;
   if (plan->mode == 1 && !whole) {
     const size_t C = (size_t)2 * (plan->r0 / 2 + 1) * (8 * (plan->r1 / 16) + 1), total = (size_t)H * C;
     hipLaunchKernelGGL(spectrum_half_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, src, kf, H, h0,
-                       plan->r0, plan->r1, last_stage_scale(plan));
+                       plan->r0, plan->r1, sc, isc);
     if (h0 + H == Htot) {
       const size_t tail = (size_t)Htot * (N - C);
       hipLaunchKernelGGL(zero_fill_kernel, dim3((unsigned)((tail + 255) / 256)), dim3(256), 0, s,
@@ -501,20 +504,21 @@ int permute_launch(const float2* src, float2* kf, int H, const sffft_plan* plan,
   } else {
     const size_t total = (size_t)H * N;
     hipLaunchKernelGGL(spectrum_permute_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, src,
-                       kf + (size_t)h0 * N, H, plan->r0, plan->r1, plan->r2, plan->mode, last_stage_scale(plan));
+                       kf + (size_t)h0 * N, H, plan->r0, plan->r1, plan->r2, plan->mode, sc, isc);
   }
   return hip_status(hipGetLastError(), "spectrum permute launch");
 }
 
 // Spectrum of the H filter rows from channel h0 on (all Htot of them when Htot < 0): kr, plus
-// i ki for a complex filter (ki non-null, whole spectrum). The padded rows are transformed
+// i ki for a complex filter (ki non-null, whole spectrum); with conj, its conjugate (the
+// spectrum the correlations of the backward passes run on). The padded rows are transformed
 // in place in `work` (H * N complex64; fp64 stages, complex64 between them), then gathered
 // into kernel order. Up to 16384 points the transform is one pass through LDS and needs no
 // workspace. Longer rows take the staged transform, whose workspace is this call's own rows
 // of kf: the gather overwrites them afterwards, and the results of earlier calls (channels
 // before h0, at most h0 * N values even as Hermitian halves) lie before them.
 int spectrum_impl(const float* kr, const float* ki, int H, int L, int klen, const sffft_plan* plan, void* kf,
-                  void* work, void* stream, int whole = 0, int h0 = 0, int Htot = -1) {
+                  void* work, void* stream, int whole = 0, int conj = 0, int h0 = 0, int Htot = -1) {
   if (!kr || !kf || !work || H < 1 || kf == work) return SFFFT_EINVAL;
   const int rc = check_shape(L, plan);
   if (rc) return rc;
@@ -529,7 +533,7 @@ int spectrum_impl(const float* kr, const float* ki, int H, int L, int klen, cons
   const xf::Seqs q{H, 1, 0, N, 1, 0};
   float2* scratch = N <= xf::ONEPASS_MAX_N ? nullptr : static_cast<float2*>(kf) + (size_t)h0 * N;
   if ((st = hip_status(xf::run(w, w, scratch, q, N, 0, 1.f, s), "spectrum transform launch"))) return st;
-  return permute_launch(w, static_cast<float2*>(kf), H, plan, whole, s, h0, Htot);
+  return permute_launch(w, static_cast<float2*>(kf), H, plan, whole, conj, s, h0, Htot);
 }
 }  // namespace
 }  // namespace sffft
@@ -613,6 +617,10 @@ int sffft_spectrum(const float* k, int H, int L, const sffft_plan* plan, void* k
   return spectrum_impl(k, nullptr, H, L, L, plan, kf, work, stream);
 }
 
+int sffft_spectrum_conj(const float* k, int H, int L, const sffft_plan* plan, void* kf, void* work, void* stream) {
+  return spectrum_impl(k, nullptr, H, L, L, plan, kf, work, stream, 0, 1);
+}
+
 int sffft_spectrum_noalloc(const float* k, int H, int L, const sffft_plan* plan, void* kf, void* stream) {
   if (!k || !kf || H < 1) return SFFFT_EINVAL;
   int rc = check_shape(L, plan);
@@ -627,7 +635,8 @@ int sffft_spectrum_noalloc(const float* k, int H, int L, const sffft_plan* plan,
   if ((rc = scratch_for_device(&work))) return rc;
   const int chunk = (int)std::min<size_t>((size_t)H, SFFFT_SCRATCH_BYTES / per);
   for (int h0 = 0; h0 < H; h0 += chunk)
-    if ((rc = spectrum_impl(k, nullptr, std::min(chunk, H - h0), L, L, plan, kf, work, stream, 0, h0, H))) return rc;
+    if ((rc = spectrum_impl(k, nullptr, std::min(chunk, H - h0), L, L, plan, kf, work, stream, 0, 0, h0, H)))
+      return rc;
   return SFFFT_OK;
 }
 
@@ -660,7 +669,8 @@ int sffft_spectrum_from_natural(const void* kc, int H, int L, const sffft_plan* 
   if (!kc || !kf || H < 1 || kc == kf) return SFFFT_EINVAL;
   const int rc = check_shape(L, plan);
   if (rc) return rc;
-  return permute_launch(static_cast<const float2*>(kc), static_cast<float2*>(kf), H, plan, 0, (hipStream_t)stream);
+  return permute_launch(static_cast<const float2*>(kc), static_cast<float2*>(kf), H, plan, 0, 0,
+                        (hipStream_t)stream);
 }
 
 int sffft_conv_f32(const float* u, const void* kf, float* y, int B, int H, int L, const sffft_plan* plan,

@@ -3,7 +3,8 @@
 // The reference names a library with a PyTorch binding as its next step (README.md:177),
 // for the long-convolution layers of Hyena/H3/S4-style models (README.md:11):
 //
-//   sffft::spectrum(Tensor k, int[] plan) -> Tensor        k [H, L] fp32 -> [H, 2L] complex64
+//   sffft::spectrum(Tensor k, int[] plan, bool conj=False) -> Tensor
+//                                    k [H, L] fp32 -> [H, 2L] complex64 (conj: its conjugate)
 //   sffft::conv(Tensor u, Tensor kf, int[] plan) -> Tensor  u [B, H, L] fp32 or bf16
 //
 // `plan` is the nine sffft_plan fields (r0, r1, r2, waves, acc, cached, seqs, mode, channels).
@@ -17,8 +18,10 @@
 // used only while tracing, stay in Python (sffft_amd/torch_ops.py).
 //
 // Gradients: sffft::conv is differentiable in u. The adjoint of causal convolution is the
-// anti-causal correlation du[m] = sum_{n >= m} dy[n] k[n - m] = flip(causal_conv(flip(dy), k)),
-// so the backward pass runs the same kernel on the same spectrum. sffft::spectrum has no
+// anti-causal correlation du[m] = sum_{n >= m} dy[n] k[n - m]. With the N = 2L zero padding
+// that is IDFT(DFT(dy) * conj(K))[m] for m < L: the same kernel on the conjugated spectrum
+// (elementwise conjugation of the kernel-order buffer is the kernel-order buffer of conj(K),
+// Hermitian halves included), with no time reversal of dy or du. sffft::spectrum has no
 // gradient; backpropagating through it raises.
 #include <ATen/ATen.h>
 #include <c10/core/DeviceGuard.h>
@@ -43,7 +46,7 @@ void check(int rc, const char* what) {
   TORCH_CHECK(rc == SFFFT_OK, what, " failed: ", sffft_strerror(rc), " (", rc, ") ", sffft_last_error());
 }
 
-at::Tensor spectrum_gpu(const at::Tensor& k_in, c10::IntArrayRef plan_fields) {
+at::Tensor spectrum_gpu(const at::Tensor& k_in, c10::IntArrayRef plan_fields, bool conj) {
   TORCH_CHECK(k_in.is_cuda() && k_in.scalar_type() == at::kFloat && k_in.dim() == 2,
               "sffft::spectrum: k must be a [H, L] float32 GPU tensor");
   // torch labels GPU tensors CUDA on this backend too; the generic guard picks the
@@ -55,7 +58,8 @@ at::Tensor spectrum_gpu(const at::Tensor& k_in, c10::IntArrayRef plan_fields) {
   const sffft_plan p = to_plan(plan_fields);
   at::Tensor kf = at::empty({H, 2 * L}, k.options().dtype(at::kComplexFloat));
   at::Tensor work = at::empty_like(kf);  // sffft_spectrum_bytes(H, L): scratch, clobbered
-  check(sffft_spectrum(k.data_ptr<float>(), (int)H, (int)L, &p, kf.data_ptr(), work.data_ptr(), current_stream()),
+  check((conj ? sffft_spectrum_conj : sffft_spectrum)(k.data_ptr<float>(), (int)H, (int)L, &p, kf.data_ptr(),
+                                                       work.data_ptr(), current_stream()),
         "sffft_spectrum");
   return kf;
 }
@@ -102,11 +106,11 @@ at::Tensor call_conv(const at::Tensor& u, const at::Tensor& kf, c10::IntArrayRef
   return op.call(u, kf, plan);
 }
 
-at::Tensor call_spectrum(const at::Tensor& k, c10::IntArrayRef plan) {
+at::Tensor call_spectrum(const at::Tensor& k, c10::IntArrayRef plan, bool conj) {
   static const auto op = c10::Dispatcher::singleton()
                              .findSchemaOrThrow("sffft::spectrum", "")
-                             .typed<at::Tensor(const at::Tensor&, c10::IntArrayRef)>();
-  return op.call(k, plan);
+                             .typed<at::Tensor(const at::Tensor&, c10::IntArrayRef, bool)>();
+  return op.call(k, plan, conj);
 }
 
 using torch::autograd::AutogradContext;
@@ -125,16 +129,16 @@ class ConvFn : public torch::autograd::Function<ConvFn> {
     const at::Tensor kf = ctx->get_saved_variables()[0];
     const std::vector<int64_t> plan = ctx->saved_data["plan"].toIntVector();
     at::Tensor du;
-    if (ctx->needs_input_grad(0)) du = call_conv(grads[0].flip({-1}).contiguous(), kf, plan).flip({-1});
+    if (ctx->needs_input_grad(0)) du = call_conv(grads[0].contiguous(), at::conj_physical(kf), plan);
     return {du, at::Tensor(), at::Tensor()};
   }
 };
 
 class SpectrumFn : public torch::autograd::Function<SpectrumFn> {
  public:
-  static at::Tensor forward(AutogradContext*, const at::Tensor& k, c10::IntArrayRef plan) {
+  static at::Tensor forward(AutogradContext*, const at::Tensor& k, c10::IntArrayRef plan, bool conj) {
     at::AutoDispatchBelowADInplaceOrView guard;
-    return call_spectrum(k, plan);
+    return call_spectrum(k, plan, conj);
   }
   static variable_list backward(AutogradContext*, variable_list) {
     TORCH_CHECK(false, "sffft::spectrum has no gradient with respect to the filter");
@@ -146,12 +150,14 @@ at::Tensor conv_autograd(const at::Tensor& u, const at::Tensor& kf, c10::IntArra
   return ConvFn::apply(u, kf, plan);
 }
 
-at::Tensor spectrum_autograd(const at::Tensor& k, c10::IntArrayRef plan) { return SpectrumFn::apply(k, plan); }
+at::Tensor spectrum_autograd(const at::Tensor& k, c10::IntArrayRef plan, bool conj) {
+  return SpectrumFn::apply(k, plan, conj);
+}
 
 }  // namespace
 
 TORCH_LIBRARY(sffft, m) {
-  m.def("spectrum(Tensor k, int[] plan) -> Tensor");
+  m.def("spectrum(Tensor k, int[] plan, bool conj=False) -> Tensor");
   m.def("conv(Tensor u, Tensor kf, int[] plan) -> Tensor");
 }
 

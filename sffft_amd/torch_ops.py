@@ -3,8 +3,8 @@
 The reference names a library with a PyTorch binding as its next step (README.md:177), for the
 long-convolution layers of Hyena/H3/S4-style models (README.md:11). This module provides it:
 
-- ``torch.ops.sffft.spectrum(k, plan)``: the kernel-order spectrum [H, 2L] complex64 of a real
-  filter k [H, L] (fp32);
+- ``torch.ops.sffft.spectrum(k, plan, conj=False)``: the kernel-order spectrum [H, 2L]
+  complex64 of a real filter k [H, L] (fp32), or its conjugate;
 - ``torch.ops.sffft.conv(u, kf, plan)``: y = causal_conv(u, k) for u [B, H, L] fp32 or bf16;
 - ``LongConv``: the two together, with the spectrum cached per (filter tensor, its version, L,
   plan), so a layer whose filter does not change computes the spectrum once.
@@ -19,12 +19,14 @@ they capture into CUDA/HIP graphs.
 Gradients:
 
 - ``conv`` is differentiable in u. Causal convolution's adjoint is the anti-causal correlation
-  du[m] = sum_{n >= m} dy[n] k[n - m], which is flip(causal_conv(flip(dy), k)): the backward pass
-  runs the same kernel on the same spectrum.
+  du[m] = sum_{n >= m} dy[n] k[n - m]. With the N = 2L zero padding this is
+  IDFT(DFT(dy) * conj(K))[m] for m < L, so the backward pass runs the same kernel on the
+  conjugated spectrum (elementwise conjugation of the kernel-order buffer), with no time
+  reversal.
 - ``LongConv`` is differentiable in u and in the filter k. The filter gradient is the
-  batch-summed correlation dk[h, j] = sum_b sum_{n >= j} dy[b, h, n] u[b, h, n - j]. Per sequence
-  this is flip(causal_conv(flip(dy), u)), with u as the filter (``filter_grad``): the B*H input
-  rows become filters of a batch-of-one convolution of the flipped output gradients.
+  batch-summed correlation dk[h, j] = sum_b sum_{n >= j} dy[b, h, n] u[b, h, n - j]: per
+  sequence the same correlation with u in the filter's place (``filter_grad``). The B*H input
+  rows become conjugated spectra of a batch-of-one convolution of the output gradients.
 - ``spectrum`` itself has no gradient and raises if its filter requires grad.
 """
 from __future__ import annotations
@@ -51,7 +53,7 @@ def plan_fields(plan: Plan) -> List[int]:
 
 
 @torch.library.register_fake("sffft::spectrum")
-def _spectrum_fake(k, plan):
+def _spectrum_fake(k, plan, conj=False):
     torch._check(k.dim() == 2, lambda: "k must be [H, L]")
     torch._check(k.dtype == torch.float32, lambda: "k must be float32")
     return k.new_empty((k.shape[0], 2 * k.shape[1]), dtype=torch.complex64)
@@ -69,21 +71,23 @@ def _conv_fake(u, kf, plan):
 def filter_grad(u: torch.Tensor, dy: torch.Tensor) -> torch.Tensor:
     """dk[h, j] = sum_b sum_{n >= j} dy[b, h, n] u[b, h, n - j] for u, dy [B, H, L] (fp32 [H, L]).
 
-    Computed on the GPU kernels as flip(causal_conv(flip(dy), u)) per sequence, summed over b:
-    the B*H rows of u are the filters (fp32 spectra) of a batch-of-one convolution. Multi-pass
-    lengths (L > 16384) take pairs of sequences only, so there each row of flip(dy) is paired
-    with a zero row (a batch of two whose second row is discarded).
+    Computed on the GPU kernels per sequence as the convolution of dy with the conjugate
+    spectrum of u (the correlation of the two; the conjugation is folded into the spectrum's
+    gather), summed over b: the B*H rows of u are the filters (fp32 spectra) of a
+    batch-of-one convolution. Multi-pass lengths (L > 16384) take
+    pairs of sequences only, so there each row of dy is paired with a zero row (a batch of two
+    whose second row is discarded).
     """
     B, H, L = u.shape
     pairs_only = L in LONG_DEFAULT_PLANS
     plan = default_plan(L, "fp32", 2 if pairs_only else 1)  # one sequence per transform: batch of one
     fields = plan_fields(plan)
-    kf = torch.ops.sffft.spectrum(u.detach().float().reshape(B * H, L).contiguous(), fields)
-    w = dy.float().flip(-1).reshape(1, B * H, L)
+    kf = torch.ops.sffft.spectrum(u.detach().float().reshape(B * H, L).contiguous(), fields, True)
+    w = dy.float().reshape(1, B * H, L)
     if pairs_only:
         w = torch.cat([w, torch.zeros_like(w)])
     r = torch.ops.sffft.conv(w.contiguous(), kf, fields)[:1]
-    return r.reshape(B, H, L).flip(-1).sum(0)
+    return r.reshape(B, H, L).sum(0)
 
 
 class _LongConvFn(torch.autograd.Function):
@@ -100,7 +104,7 @@ class _LongConvFn(torch.autograd.Function):
         u, kf = ctx.saved_tensors
         du = dk = None
         if ctx.needs_input_grad[0]:
-            du = torch.ops.sffft.conv(dy.flip(-1).contiguous().to(u.dtype), kf, ctx.fields).flip(-1)
+            du = torch.ops.sffft.conv(dy.to(u.dtype).contiguous(), torch.conj_physical(kf), ctx.fields)
         if ctx.needs_input_grad[1]:
             dk = filter_grad(u, dy)
         return du, dk, None, None

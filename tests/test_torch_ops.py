@@ -1,8 +1,9 @@
 """The PyTorch operators over the C ABI (sffft_amd/torch_ops.py).
 
-CPU: schemas, fake-tensor shape propagation, the tuned default plans, and the identity behind
-the input gradient (the adjoint of causal convolution is flip o causal_conv o flip), checked on
-the fp64 oracle against a brute-force anti-causal correlation.
+CPU: schemas, fake-tensor shape propagation, the tuned default plans, and the identities behind
+the gradients (the adjoint of causal convolution is flip o causal_conv o flip, and equally the
+same convolution with the conjugate spectrum, which the backward passes run), checked against
+brute-force anti-causal correlations.
 GPU: bit equality with the C-ABI path, torch.library.opcheck, the gradient against the oracle,
 the spectrum cache, torch.compile and graph capture.
 """
@@ -20,7 +21,8 @@ from sffft_amd import torch_ops
 
 def test_schemas():
     assert str(torch.ops.sffft.conv.default._schema) == "sffft::conv(Tensor u, Tensor kf, int[] plan) -> Tensor"
-    assert str(torch.ops.sffft.spectrum.default._schema) == "sffft::spectrum(Tensor k, int[] plan) -> Tensor"
+    assert str(torch.ops.sffft.spectrum.default._schema) == \
+        "sffft::spectrum(Tensor k, int[] plan, bool conj=False) -> Tensor"
     # registered from C++ (libsffft_torch.so): GPU kernels and autograd, no Python wrapper
     for op in (torch.ops.sffft.conv.default, torch.ops.sffft.spectrum.default):
         assert torch._C._dispatch_has_kernel_for_dispatch_key(op.name(), "CUDA")
@@ -69,6 +71,25 @@ def test_adjoint_is_flipped_causal_convolution():
     assert np.abs(wrong - du).max() > 1e-3 * np.abs(du).max()
 
 
+def test_correlation_is_convolution_with_the_conjugate_spectrum():
+    """The adjoint the backward passes run: with N = 2L zero padding,
+    sum_{n >= m} x[n] k[n - m] = IDFT_N(DFT_N(x) * conj(DFT_N(k)))[m] for m < L, i.e. the causal
+    convolution machinery with the filter's spectrum conjugated (no time reversal)."""
+    rng = np.random.default_rng(9)
+    L = 40
+    N = 2 * L
+    x = rng.standard_normal(L)
+    k = rng.standard_normal(L)
+    corr = np.array([sum(x[n] * k[n - m] for n in range(m, L)) for m in range(L)])
+    X = np.fft.fft(x, N)
+    K = np.fft.fft(k, N)
+    got = np.fft.ifft(X * np.conj(K))[:L]
+    assert np.abs(got.imag).max() < 1e-12 and np.abs(got.real - corr).max() < 1e-12 * np.abs(corr).max()
+    # the plain spectrum gives the causal convolution instead (the mistake this guards against)
+    wrong = np.fft.ifft(X * K)[:L].real
+    assert np.abs(wrong - corr).max() > 1e-3 * np.abs(corr).max()
+
+
 def test_filter_gradient_is_flipped_causal_convolution():
     """dk[h,j] = sum_b sum_{n>=j} dy[b,h,n] u[b,h,n-j] equals flip(causal_conv(flip(dy), u))
     summed over b, with u as a per-sequence filter: the identity filter_grad runs on."""
@@ -100,7 +121,7 @@ def _inputs(dev, B, H, L, seed):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("L,io", [(1024, "fp32"), (4096, "bf16")])
+@pytest.mark.parametrize("L,io", [(1024, "fp32"), (4096, "bf16"), (32768, "fp32")])
 def test_ops_match_the_c_abi(dev, L, io):
     u, k, _, _ = _inputs(dev, 4, 13, L, seed=L)
     if io == "bf16":
@@ -110,6 +131,9 @@ def test_ops_match_the_c_abi(dev, L, io):
     kf = torch.ops.sffft.spectrum(k, p)
     assert torch.equal(torch.view_as_real(kf), torch.view_as_real(sf.spectrum(k, L, plan)))
     assert torch.equal(torch.ops.sffft.conv(u, kf, p), sf.conv(u, kf, plan))
+    # the conjugate spectrum is the conjugate of the spectrum, value for value
+    kc = torch.ops.sffft.spectrum(k, p, True)
+    assert torch.equal(torch.view_as_real(kc), torch.view_as_real(torch.conj_physical(kf)))
 
 
 @pytest.mark.gpu
@@ -118,6 +142,7 @@ def test_opcheck(dev):
     p = torch_ops.plan_fields(sf.default_plan(256, "fp32", 2))
     kf = torch.ops.sffft.spectrum(k, p)
     torch.library.opcheck(torch.ops.sffft.spectrum.default, (k, p))
+    torch.library.opcheck(torch.ops.sffft.spectrum.default, (k, p, True))
     torch.library.opcheck(torch.ops.sffft.conv.default, (u, kf, p))
     torch.library.opcheck(torch.ops.sffft.conv.default, (u.clone().requires_grad_(), kf, p))
 
