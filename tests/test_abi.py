@@ -56,6 +56,12 @@ def test_plan_validation():
     assert sf.lds_bytes(1024, P("64x32", 12, seqs=2, mode=1, channels=3)) == (32768 + 8192 + 32768 +
                                                                             (3 * half + 1023) // 1024 * 1024 +
                                                                             12 * 16 * 36 * 4)
+    # 64x64, 12 wavefronts, 3 channels: both fragment kinds (32 KB) do not fit beside the
+    # spectra, the first kind (16 KB) does; one shared twiddle table
+    half = 33 * 33 * 16
+    assert sf.lds_bytes(2048, P("64x64", 12, seqs=2, mode=1, channels=3)) == (16384 + 32768 +
+                                                                            (3 * half + 1023) // 1024 * 1024 +
+                                                                            12 * 16 * 68 * 4) == 154624
     assert sf.lds_bytes(1024, P("64x16", 4)) == 0
 
 

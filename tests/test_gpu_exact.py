@@ -7,7 +7,10 @@
 - the half spectrum of a wave plan equals, value for value, the whole spectrum that
   sffft_spectrum_complex writes for the same real filter and a zero imaginary part;
 - sffft_to_bf16 (src/sffft.cu:306,364) against IEEE round-to-nearest-even on a bit
-  pattern sweep, ties, overflow, infinities and NaNs.
+  pattern sweep, ties, overflow, infinities and NaNs;
+- the device DFT coefficient table (the cached DFT matrices, src/sffft.cu:349-362): every
+  complex and real-input fragment against fp16(fp32(cos)), fp16(fp32(sin)) of the exact
+  angle from numpy.
 """
 import numpy as np
 import pytest
@@ -183,3 +186,44 @@ def test_to_bf16_round_to_nearest_even(dev):
     assert np.array_equal(y[~nan], want[~nan])
     yn = y[nan]
     assert np.all((yn & 0x7F80) == 0x7F80) and np.all((yn & 0x007F) != 0), "NaN stays NaN"
+
+
+
+def test_dft_table_fragments():
+    """CF[R][a][b][kind] lane (r, g) slot v holds [cos t | sin t] (kind 0) or [-sin t | cos t]
+    (kind 1) of t = 2 pi ((16a + r)(16b + 4g + v) mod R) / R; RI[R][nt][kind] lane (c, g)
+    slot j holds cos t (kind 0) or -sin t (kind 1) of t = 2 pi (n0 (16nt + c) mod R) / R,
+    n0 = 4g + j (j < 4) or 16 + 4g + j - 4, and zero for n0 >= R/2. Each value is rounded to
+    fp32 and then to fp16, as in the reference's table (src/sffft.cu:349-362). The second
+    kind's -sin is the rounded sin with its sign bit flipped, which the wave pipeline's
+    first-kind-only layout relies on."""
+    t = sf.dft_table().reshape(-1, 8)  # units of one lane's 8 halves
+    assert t.shape[0] == 3584
+    lane = np.arange(64)
+    r, g = lane & 15, lane >> 4
+
+    def h(x):
+        return x.astype(np.float32).astype(np.float16).view(np.uint16)
+
+    for R, cf, ri in ((16, 0, 128), (32, 256, 768), (64, 1024, 3072)):
+        T = R // 16
+        for a in range(T):
+            for b in range(T):
+                f = a * T + b
+                e = ((16 * a + r)[:, None] * (16 * b + 4 * g[:, None] + np.arange(4)[None])) % R
+                c, sn = h(np.cos(2 * np.pi * e / R)), h(np.sin(2 * np.pi * e / R))
+                k0 = t[cf + 2 * f * 64: cf + 2 * f * 64 + 64]
+                k1 = t[cf + (2 * f + 1) * 64: cf + (2 * f + 1) * 64 + 64]
+                np.testing.assert_array_equal(k0[:, :4], c)
+                np.testing.assert_array_equal(k0[:, 4:], sn)
+                np.testing.assert_array_equal(k1[:, :4], sn ^ 0x8000)
+                np.testing.assert_array_equal(k1[:, 4:], c)
+        j = np.arange(8)
+        n0 = np.where(j < 4, 4 * g[:, None] + j[None], 16 + 4 * g[:, None] + j[None] - 4)
+        for nt in range(T):
+            e = (n0 * (16 * nt + r)[:, None]) % R
+            zero = n0 >= R // 2
+            c = np.where(zero, 0, h(np.cos(2 * np.pi * e / R)))
+            msn = np.where(zero, 0, h(np.sin(2 * np.pi * e / R)) ^ 0x8000)
+            np.testing.assert_array_equal(t[ri + 2 * nt * 64: ri + 2 * nt * 64 + 64], c)
+            np.testing.assert_array_equal(t[ri + (2 * nt + 1) * 64: ri + (2 * nt + 1) * 64 + 64], msn)
