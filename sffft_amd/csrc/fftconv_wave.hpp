@@ -44,6 +44,11 @@
 #pragma once
 #include "fftconv.hpp"
 
+// k0 strips per phase-2 step when the DFT fragments are read from LDS (not held)
+#ifndef SFFFT_WAVE_STRIPS
+#define SFFFT_WAVE_STRIPS 2
+#endif
+
 namespace sffft {
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
@@ -416,39 +421,61 @@ __device__ __forceinline__ void process_pair(const PairLoads<P, TIO>& d, TIO* S,
     if constexpr (HOLD_F1) return g0[i][k][kind];
     else return dft_frag<P::R1, K1>(F1, i, k, kind, lane);
   };
+  // Strips are taken SG at a time, so that each DFT fragment read from LDS (and, with
+  // the first kind only, each second kind rebuilt from it) serves SG strips: without
+  // held fragments phase 2 is bound by these LDS reads. The accumulation order of every
+  // output is the same for any SG.
+  constexpr int SG = HOLD_F1 ? 1 : SFFFT_WAVE_STRIPS;
+  static_assert(ST % SG == 0, "whole strip groups");
 #pragma unroll
-  for (int s = 0; s < ST; s++) {
-    h8 a2[MT];
+  for (int s0 = 0; s0 < ST; s0 += SG) {
+    h8 a2[SG][MT];
 #pragma unroll
     for (int kt = 0; kt < MT; kt++) {
       step_fence();
-      f4 dr = {0.f, 0.f, 0.f, 0.f}, di = {0.f, 0.f, 0.f, 0.f};
+      f4 dr[SG], di[SG];
+#pragma unroll
+      for (int j = 0; j < SG; j++) dr[j] = di[j] = (f4){0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int mt = 0; mt < MT; mt++) {
-        dr = mfma(f1frag(kt, mt, 0), b2[mt][s], dr);
-        di = mfma(f1frag(kt, mt, 1), b2[mt][s], di);
+        const h8 fa = f1frag(kt, mt, 0), fb = f1frag(kt, mt, 1);
+#pragma unroll
+        for (int j = 0; j < SG; j++) {
+          dr[j] = mfma(fa, b2[mt][s0 + j], dr[j]);
+          di[j] = mfma(fb, b2[mt][s0 + j], di[j]);
+        }
       }
-      dr = acc_round<ACC16>(dr);
-      di = acc_round<ACC16>(di);
-      const int tile = s * MT + kt;
-      if constexpr (HERM)
-        a2[kt] = herm_spectrum_pack<P>(dr, di, SP, s, kt, lane);
-      else
-        a2[kt] = spectrum_conj_pack(dr, di, SP[sp_index(tile, lane, 0)], SP[sp_index(tile, lane, 1)]);
+#pragma unroll
+      for (int j = 0; j < SG; j++) {
+        const int s = s0 + j, tile = s * MT + kt;
+        const f4 r = acc_round<ACC16>(dr[j]), i = acc_round<ACC16>(di[j]);
+        if constexpr (HERM)
+          a2[j][kt] = herm_spectrum_pack<P>(r, i, SP, s, kt, lane);
+        else
+          a2[j][kt] = spectrum_conj_pack(r, i, SP[sp_index(tile, lane, 0)], SP[sp_index(tile, lane, 1)]);
+      }
     }
 #pragma unroll
     for (int t = 0; t < MT; t++) {
       step_fence();
-      f4 er = {0.f, 0.f, 0.f, 0.f}, ei = {0.f, 0.f, 0.f, 0.f};
+      f4 er[SG], ei[SG];
+#pragma unroll
+      for (int j = 0; j < SG; j++) er[j] = ei[j] = (f4){0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int kt = 0; kt < MT; kt++) {
-        er = mfma(a2[kt], f1frag(t, kt, 0), er);
-        ei = mfma(a2[kt], f1frag(t, kt, 1), ei);
+        const h8 fa = f1frag(t, kt, 0), fb = f1frag(t, kt, 1);
+#pragma unroll
+        for (int j = 0; j < SG; j++) {
+          er[j] = mfma(a2[j][kt], fa, er[j]);
+          ei[j] = mfma(a2[j][kt], fb, ei[j]);
+        }
       }
-      er = acc_round<ACC16>(er);
-      ei = acc_round<ACC16>(ei);
-      const int tt = s * MT + t;
-      b2[t][s] = cmul_pack(er, ei, TW2[tw_index(tt, lane, 0)], TW2[tw_index(tt, lane, 1)]);
+#pragma unroll
+      for (int j = 0; j < SG; j++) {
+        const int tt = (s0 + j) * MT + t;
+        b2[t][s0 + j] = cmul_pack(acc_round<ACC16>(er[j]), acc_round<ACC16>(ei[j]), TW2[tw_index(tt, lane, 0)],
+                                  TW2[tw_index(tt, lane, 1)]);
+      }
     }
   }
 

@@ -45,6 +45,11 @@
 #pragma once
 #include "fftconv_wave.hpp"
 
+// k0 strips per phase-2 step of the row pass (pass B)
+#ifndef LONG_ROW_STRIPS
+#define LONG_ROW_STRIPS 2
+#endif
+
 namespace sffft {
 
 constexpr int LC_COLS = 64;   // columns of a wavefront in the column passes (four 16-wide tiles)
@@ -266,33 +271,55 @@ __device__ __forceinline__ void long_row(uint32_t* x, const float4* __restrict__
     }
   }
 
-  // ---- phase 2: per k0 strip, DFT over n1, spectrum, inverse DFT over k1, twiddle
+  // ---- phase 2: per k0 strip, DFT over n1, spectrum, inverse DFT over k1, twiddle.
+  // Strips are taken SG at a time, so that each DFT fragment read from LDS (and its
+  // second kind rebuilt in registers) serves SG strips; the accumulation order of every
+  // output is the same for any SG.
+  constexpr int SG = ST % LONG_ROW_STRIPS == 0 ? LONG_ROW_STRIPS : 1;
 #pragma unroll
-  for (int s = 0; s < ST; s++) {
-    h8 a2[MT];
+  for (int s0 = 0; s0 < ST; s0 += SG) {
+    h8 a2[SG][MT];
 #pragma unroll
     for (int kt = 0; kt < MT; kt++) {
       step_fence();
-      f4 dr = {0.f, 0.f, 0.f, 0.f}, di = {0.f, 0.f, 0.f, 0.f};
+      f4 dr[SG], di[SG];
+#pragma unroll
+      for (int j = 0; j < SG; j++) dr[j] = di[j] = (f4){0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int mt = 0; mt < MT; mt++) {
-        dr = mfma(dft_frag<R1, true>(F1, kt, mt, 0, lane), b2[mt][s], dr);
-        di = mfma(dft_frag<R1, true>(F1, kt, mt, 1, lane), b2[mt][s], di);
+        const h8 fa = dft_frag<R1, true>(F1, kt, mt, 0, lane), fb = dft_frag<R1, true>(F1, kt, mt, 1, lane);
+#pragma unroll
+        for (int j = 0; j < SG; j++) {
+          dr[j] = mfma(fa, b2[mt][s0 + j], dr[j]);
+          di[j] = mfma(fb, b2[mt][s0 + j], di[j]);
+        }
       }
-      const int tile = s * MT + kt;
-      a2[kt] = spectrum_conj_pack(dr, di, SP[sp_index(tile, lane, 0)], SP[sp_index(tile, lane, 1)]);
+#pragma unroll
+      for (int j = 0; j < SG; j++) {
+        const int tile = (s0 + j) * MT + kt;
+        a2[j][kt] = spectrum_conj_pack(dr[j], di[j], SP[sp_index(tile, lane, 0)], SP[sp_index(tile, lane, 1)]);
+      }
     }
 #pragma unroll
     for (int t = 0; t < MT; t++) {
       step_fence();
-      f4 er = {0.f, 0.f, 0.f, 0.f}, ei = {0.f, 0.f, 0.f, 0.f};
+      f4 er[SG], ei[SG];
+#pragma unroll
+      for (int j = 0; j < SG; j++) er[j] = ei[j] = (f4){0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int kt = 0; kt < MT; kt++) {
-        er = mfma(a2[kt], dft_frag<R1, true>(F1, t, kt, 0, lane), er);
-        ei = mfma(a2[kt], dft_frag<R1, true>(F1, t, kt, 1, lane), ei);
+        const h8 fa = dft_frag<R1, true>(F1, t, kt, 0, lane), fb = dft_frag<R1, true>(F1, t, kt, 1, lane);
+#pragma unroll
+        for (int j = 0; j < SG; j++) {
+          er[j] = mfma(a2[j][kt], fa, er[j]);
+          ei[j] = mfma(a2[j][kt], fb, ei[j]);
+        }
       }
-      const int tt = s * MT + t;
-      b2[t][s] = cmul_pack(er, ei, TW2[tw_index(tt, lane, 0)], TW2[tw_index(tt, lane, 1)]);
+#pragma unroll
+      for (int j = 0; j < SG; j++) {
+        const int tt = (s0 + j) * MT + t;
+        b2[t][s0 + j] = cmul_pack(er[j], ei[j], TW2[tw_index(tt, lane, 0)], TW2[tw_index(tt, lane, 1)]);
+      }
     }
   }
 
