@@ -9,6 +9,7 @@
 #include <limits>
 #include <map>
 #include <mutex>
+#include <tuple>
 #include <vector>
 
 #include "../../include/sffft.h"
@@ -200,10 +201,12 @@ int device_table(const void** out) {
 // ---- twiddle tables of the wave pipeline (fftconv_wave.hpp) ---------------------
 // TW1[tile mt*ST+nt][lane (c,g)][v] = sc0 * w^(m k0),        m = 16mt+4g+v, k0 = 16nt+c
 // TW2[tile s*MT+t][lane (c,g)][v]   = sc0 * sc1 * w^(k0 n1), k0 = 16s+4g+v,  n1 = 16t+c
+// (complex fp32, at float4 tw_index(split, tile, lane, v / 2), slot v % 2: the wave pipeline's
+// layout is tw_split(r0, r1), the multi-pass row pass's the paired one)
 // with w = exp(-2 pi i / N), sc = 1/sqrt(R); exponents reduced mod N, fp64 then fp32.
 // Square plans (r0 == r1) read TW1 only: TW2 equals it index for index up to sc1,
 // which their spectrum carries instead (last_stage_scale).
-void build_twiddles(int r0, int r1, std::vector<float>& t) {
+void build_twiddles(int r0, int r1, bool split, std::vector<float>& t) {
   const int N = r0 * r1, ST = r0 / 16, MT = r1 / 16;
   const double two_pi = 6.283185307179586476925286766559;
   const double sc0 = 1.0 / std::sqrt((double)r0), sc1 = 1.0 / std::sqrt((double)r1);
@@ -212,7 +215,7 @@ void build_twiddles(int r0, int r1, std::vector<float>& t) {
     e %= N;
     if (e > N / 2) e -= N;
     const double a = two_pi * (double)e / (double)N;
-    float* f = &t[base + ((size_t)tile * 64 + lane) * 8 + 2 * v];
+    float* f = &t[base + (size_t)tw_index(split, tile, lane, v / 2) * 4 + 2 * (v % 2)];
     f[0] = (float)(sc * std::cos(a));
     f[1] = (float)(-sc * std::sin(a));
   };
@@ -253,18 +256,18 @@ int scratch_for_device(void** out) {
 }
 
 std::mutex g_tw_mu;
-std::map<std::pair<int, int>, void*> g_tw[256];  // per device: (r0, r1) -> table
+std::map<std::tuple<int, int, bool>, void*> g_tw[256];  // per device: (r0, r1, split) -> table
 
-int device_twiddles(int r0, int r1, const void** out) {
+int device_twiddles(int r0, int r1, bool split, const void** out) {
   int dev = 0;
   hipError_t err = hipGetDevice(&dev);
   if (err != hipSuccess) return hip_status(err, "hipGetDevice");
   if (dev < 0 || dev >= 256) return SFFFT_EINVAL;
   std::lock_guard<std::mutex> lock(g_tw_mu);
-  void*& slot = g_tw[dev][std::make_pair(r0, r1)];
+  void*& slot = g_tw[dev][std::make_tuple(r0, r1, split)];
   if (!slot) {
     std::vector<float> host;
-    build_twiddles(r0, r1, host);
+    build_twiddles(r0, r1, split, host);
     void* d = nullptr;
     if ((err = hipMalloc(&d, host.size() * sizeof(float))) != hipSuccess) return hip_status(err, "hipMalloc");
     if ((err = hipMemcpy(d, host.data(), host.size() * sizeof(float), hipMemcpyHostToDevice)) != hipSuccess) {
@@ -417,7 +420,7 @@ int conv(const void* u, const void* kf, void* y, int B, int H, int L, const sfff
   const void* table = nullptr;
   if ((rc = device_table(&table))) return rc;
   const void* tw = nullptr;
-  if (e->mode == 1 && (rc = device_twiddles(p->r0, p->r1, &tw))) return rc;
+  if (e->mode == 1 && (rc = device_twiddles(p->r0, p->r1, tw_split(p->r0, p->r1), &tw))) return rc;
   const launch_fn fn = cplx && e->mode == 1 ? e->launch_complex[IO][p->cached] : e->launch[IO][p->cached];
   return hip_status(fn(u, kf, y, B, H, table, tw, p->acc, (hipStream_t)stream), "fused convolution launch");
 }
@@ -465,7 +468,7 @@ int conv_long(const void* u, const void* kf, void* y, void* work, size_t wbytes,
   const void* table = nullptr;
   if ((rc = device_table(&table))) return rc;
   const void* tw = nullptr;
-  if ((rc = device_twiddles(p->r1, p->r2, &tw))) return rc;
+  if ((rc = device_twiddles(p->r1, p->r2, false, &tw))) return rc;
   return hip_status(e->launch[circ][IO](u, kf, y, work, B, H, chunk, table, tw, (hipStream_t)stream),
                     "multi-pass launch");
 }

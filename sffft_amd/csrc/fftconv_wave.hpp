@@ -99,7 +99,16 @@ struct WavePlan {
 };
 
 // Twiddle-table index of lane `lane`, tile (a, b), float4 q (q = 0: values 0,1; q = 1: 2,3).
-__host__ __device__ constexpr int tw_index(int tile, int lane, int q) { return (tile * 64 + lane) * 2 + q; }
+// Split layout: each float4 of a tile in its own run of 64 lanes, so that the lanes of one
+// 16-byte read are 16 bytes apart and fall on distinct banks. Paired layout: both float4 of
+// a lane side by side; lanes are 32 bytes apart, and lanes l and l+4 of every 8-lane pass
+// share banks (two-way conflicts on every twiddle read, all of the kernel's conflicts). The
+// paired layout is kept for 64x64, whose 168-VGPR kernel spills with the split one (its
+// two reads per tile then need two lane offsets): 5% slower there, 3% faster at 64x32.
+__host__ __device__ constexpr bool tw_split(int r0, int r1) { return !(r0 == 64 && r1 == 64); }
+__host__ __device__ constexpr int tw_index(bool split, int tile, int lane, int q) {
+  return split ? (tile * 2 + q) * 64 + lane : (tile * 64 + lane) * 2 + q;
+}
 // Spectrum index (float4 units) in the wave pipeline's order: tile = s*MT + kt,
 // q as above; lanes at 16-byte stride so one load instruction reads 1 KB.
 __host__ __device__ constexpr int sp_index(int tile, int lane, int q) { return (tile * 2 + q) * 64 + lane; }
@@ -371,6 +380,7 @@ __device__ __forceinline__ void process_pair(const PairLoads<P, TIO>& d, TIO* S,
                                              TIO* __restrict__ ya, TIO* __restrict__ yb, const h8* F0,
                                              const h8* F1, const float4* TW1, const float4* TW2, int lane) {
   constexpr int R0 = P::R0, M = P::M, MT = P::MT, ST = P::ST, KS1 = P::KS1, NT3 = P::NT3;
+  constexpr bool TWS = tw_split(P::R0, P::R1);  // twiddle-table layout (tw_index)
   // With 16 tiles per transform (64x64) the pair alone fills 64 VGPRs; compiler-only
   // barriers at the top of each tile step keep the next step's table and spectrum
   // loads from being hoisted over the current one, which would not fit beside it.
@@ -403,7 +413,7 @@ __device__ __forceinline__ void process_pair(const PairLoads<P, TIO>& d, TIO* S,
       dr = acc_round<ACC16>(dr);
       di = acc_round<ACC16>(di);
       const int t = mt * ST + nt;
-      b2[mt][nt] = cmul_pack(dr, di, TW1[tw_index(t, lane, 0)], TW1[tw_index(t, lane, 1)]);
+      b2[mt][nt] = cmul_pack(dr, di, TW1[tw_index(TWS, t, lane, 0)], TW1[tw_index(TWS, t, lane, 1)]);
     }
   }
 
@@ -473,8 +483,8 @@ __device__ __forceinline__ void process_pair(const PairLoads<P, TIO>& d, TIO* S,
 #pragma unroll
       for (int j = 0; j < SG; j++) {
         const int tt = (s0 + j) * MT + t;
-        b2[t][s0 + j] = cmul_pack(acc_round<ACC16>(er[j]), acc_round<ACC16>(ei[j]), TW2[tw_index(tt, lane, 0)],
-                                  TW2[tw_index(tt, lane, 1)]);
+        b2[t][s0 + j] = cmul_pack(acc_round<ACC16>(er[j]), acc_round<ACC16>(ei[j]), TW2[tw_index(TWS, tt, lane, 0)],
+                                  TW2[tw_index(TWS, tt, lane, 1)]);
       }
     }
   }
