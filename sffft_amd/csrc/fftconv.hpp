@@ -53,6 +53,11 @@
 #define SFFFT_FP32_SPLITS 8
 #endif
 
+// k0 rows per phase-2 step of three-stage plans (each wavefront's rows taken this many at a time)
+#ifndef SFFFT_WG_ROWS
+#define SFFFT_WG_ROWS 2
+#endif
+
 namespace sffft {
 
 typedef _Float16 h4 __attribute__((ext_vector_type(4)));
@@ -663,14 +668,18 @@ __device__ __forceinline__ void phase2_s3(_Float16* re, _Float16* im, const floa
   // (double-buffered); otherwise at the start of their own row, in flight while the
   // stage over n1 runs.
   constexpr int KQB = T1 * T2 == 1 && ROWS > 1 ? 2 : 1;
-  float4 kq[KQB][T1][T2][2];
+  // rows per step (RP below): plans with one 16x16 tile per row only; with more tiles per
+  // row, two rows at a time took more VGPRs than the occupancy allows (L = 8192: 13-15%
+  // slower) or gained nothing (L = 16384: 2% slower)
+  constexpr int RPK = T1 * T2 == 1 && ROWS % SFFFT_WG_ROWS == 0 ? SFFFT_WG_ROWS : 1;
+  float4 kq[RPK > 1 ? RPK : KQB][T1][T2][2];
   auto load_row_spectrum = [&](int k0, float4 (*q)[T2][2]) {
 #pragma unroll
     for (int t1 = 0; t1 < T1; t1++)
 #pragma unroll
       for (int mt = 0; mt < T2; mt++) load_k4(K + (size_t)((k0 * T1 + t1) * T2 + mt) * 256, lane, q[t1][mt]);
   };
-  if constexpr (KQB == 2) load_row_spectrum(wave * ROWS, kq[0]);
+  if constexpr (KQB == 2 && RPK == 1) load_row_spectrum(wave * ROWS, kq[0]);
   // The last twiddles of consecutive rows, w^(k0 m) and w^((k0 + 1) m), differ by the
   // factor w^m: with one tile per axis the wavefront evaluates the first row's and the
   // factors once, and steps from row to row with one complex product per value. It holds
@@ -683,115 +692,248 @@ __device__ __forceinline__ void phase2_s3(_Float16* re, _Float16* im, const floa
     twiddle4e<N>(wave * ROWS * m0, wave * ROWS * R2, sc1, lr, li);
     twiddle4e<N>(m0, R2, 1.f, fr, fi);
   }
+  if constexpr (RPK == 1) {
 #pragma unroll
-  for (int i = 0; i < ROWS; i++) {
-    const int k0 = wave * ROWS + i;  // each wavefront owns ROWS consecutive rows
-    const int rb = k0 * P::ROW;
-    if constexpr (KQB == 2) {
-      if (i + 1 < ROWS) load_row_spectrum(k0 + 1, kq[(i + 1) & 1]);
-    } else {
-      load_row_spectrum(k0, kq[0]);
-    }
-    // stage over n1: A[n2][n1] from the row's [n2 ^ (k0 & 15)][n1] block
-    h8 b[T1][T2][1 + SB];  // [k1 tile][n2 tile][hi, lo]: B operands of the stage over n2
-    {
-      h8 a[T2][T1];
+    for (int i = 0; i < ROWS; i++) {
+      const int k0 = wave * ROWS + i;  // each wavefront owns ROWS consecutive rows
+      const int rb = k0 * P::ROW;
+      if constexpr (KQB == 2) {
+        if (i + 1 < ROWS) load_row_spectrum(k0 + 1, kq[(i + 1) & 1]);
+      } else {
+        load_row_spectrum(k0, kq[0]);
+      }
+      // stage over n1: A[n2][n1] from the row's [n2 ^ (k0 & 15)][n1] block
+      h8 b[T1][T2][1 + SB];  // [k1 tile][n2 tile][hi, lo]: B operands of the stage over n2
+      {
+        h8 a[T2][T1];
 #pragma unroll
-      for (int t2 = 0; t2 < T2; t2++)
+        for (int t2 = 0; t2 < T2; t2++)
 #pragma unroll
-        for (int ks = 0; ks < T1; ks++)
-          a[t2][ks] = lds_frag(re, im, rb + (16 * t2 + (c ^ (k0 & 15))) * P::PA + 16 * ks + 4 * g);
+          for (int ks = 0; ks < T1; ks++)
+            a[t2][ks] = lds_frag(re, im, rb + (16 * t2 + (c ^ (k0 & 15))) * P::PA + 16 * ks + 4 * g);
 #pragma unroll
-      for (int t2 = 0; t2 < T2; t2++) {
+        for (int t2 = 0; t2 < T2; t2++) {
 #pragma unroll
-        for (int nt = 0; nt < T1; nt++) {
-          f4 dr = {0.f, 0.f, 0.f, 0.f}, di = {0.f, 0.f, 0.f, 0.f};
+          for (int nt = 0; nt < T1; nt++) {
+            f4 dr = {0.f, 0.f, 0.f, 0.f}, di = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-          for (int ks = 0; ks < T1; ks++) {
-            dr = mfma(a[t2][ks], f1(nt, ks, 0), dr);
-            di = mfma(a[t2][ks], f1(nt, ks, 1), di);
+            for (int ks = 0; ks < T1; ks++) {
+              dr = mfma(a[t2][ks], f1(nt, ks, 0), dr);
+              di = mfma(a[t2][ks], f1(nt, ks, 1), di);
+            }
+            dr = round_acc(dr, acc16);
+            di = round_acc(di, acc16);
+            float wr[4], wi[4], xr[4], xi[4];
+            tw_n1(nt, t2, sc1, wr, wi);
+            twiddle(dr, di, wr, wi, xr, xi);
+            pack_operand<SB != 0>(xr, xi, b[nt][t2][0], b[nt][t2][SB]);
           }
-          dr = round_acc(dr, acc16);
-          di = round_acc(di, acc16);
-          float wr[4], wi[4], xr[4], xi[4];
-          tw_n1(nt, t2, sc1, wr, wi);
-          twiddle(dr, di, wr, wi, xr, xi);
-          pack_operand<SB != 0>(xr, xi, b[nt][t2][0], b[nt][t2][SB]);
         }
       }
-    }
-    // stage over n2, spectrum, inverse over k2
-    h8 e[T2][T1][1 + SE];  // [n2 tile][k1 tile][hi, lo]: B operands of the inverse over k1
+      // stage over n2, spectrum, inverse over k2
+      h8 e[T2][T1][1 + SE];  // [n2 tile][k1 tile][hi, lo]: B operands of the inverse over k1
 #pragma unroll
-    for (int t1 = 0; t1 < T1; t1++) {
-      f4 dr[T2], di[T2];
-#pragma unroll
-      for (int mt = 0; mt < T2; mt++) {
-        dr[mt] = (f4){0.f, 0.f, 0.f, 0.f};
-        di[mt] = (f4){0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int ks = 0; ks < T2; ks++)
-#pragma unroll
-          for (int p = 0; p <= SB; p++) {
-            dr[mt] = mfma(f2(mt, ks, 0), b[t1][ks][p], dr[mt]);
-            di[mt] = mfma(f2(mt, ks, 1), b[t1][ks][p], di[mt]);
-          }
-        dr[mt] = round_acc(dr[mt], acc16);
-        di[mt] = round_acc(di[mt], acc16);
-      }
-      h8 a2[T2], a2lo[SA ? T2 : 1];
-      spectrum_product<T2, SA>(dr, di, kq[KQB == 2 ? i & 1 : 0][t1], a2, a2lo);
-#pragma unroll
-      for (int nt = 0; nt < T2; nt++) {
-        f4 er = {0.f, 0.f, 0.f, 0.f}, ei = {0.f, 0.f, 0.f, 0.f};
+      for (int t1 = 0; t1 < T1; t1++) {
+        f4 dr[T2], di[T2];
 #pragma unroll
         for (int mt = 0; mt < T2; mt++) {
-          er = mfma(a2[mt], f2(nt, mt, 0), er);
-          ei = mfma(a2[mt], f2(nt, mt, 1), ei);
-          if constexpr (SA) {
-            er = mfma(a2lo[mt], f2(nt, mt, 0), er);
-            ei = mfma(a2lo[mt], f2(nt, mt, 1), ei);
-          }
+          dr[mt] = (f4){0.f, 0.f, 0.f, 0.f};
+          di[mt] = (f4){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int ks = 0; ks < T2; ks++)
+#pragma unroll
+            for (int p = 0; p <= SB; p++) {
+              dr[mt] = mfma(f2(mt, ks, 0), b[t1][ks][p], dr[mt]);
+              di[mt] = mfma(f2(mt, ks, 1), b[t1][ks][p], di[mt]);
+            }
+          dr[mt] = round_acc(dr[mt], acc16);
+          di[mt] = round_acc(di[mt], acc16);
         }
-        er = round_acc(er, acc16);
-        ei = round_acc(ei, acc16);
-        float wr[4], wi[4], xr[4], xi[4];
-        tw_n1(nt, t1, sc2, wr, wi);
-        twiddle(er, ei, wr, wi, xr, xi);
-        pack_operand<SE != 0>(xr, xi, e[nt][t1][0], e[nt][t1][SE]);
+        h8 a2[T2], a2lo[SA ? T2 : 1];
+        spectrum_product<T2, SA>(dr, di, kq[KQB == 2 ? i & 1 : 0][t1], a2, a2lo);
+#pragma unroll
+        for (int nt = 0; nt < T2; nt++) {
+          f4 er = {0.f, 0.f, 0.f, 0.f}, ei = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int mt = 0; mt < T2; mt++) {
+            er = mfma(a2[mt], f2(nt, mt, 0), er);
+            ei = mfma(a2[mt], f2(nt, mt, 1), ei);
+            if constexpr (SA) {
+              er = mfma(a2lo[mt], f2(nt, mt, 0), er);
+              ei = mfma(a2lo[mt], f2(nt, mt, 1), ei);
+            }
+          }
+          er = round_acc(er, acc16);
+          ei = round_acc(ei, acc16);
+          float wr[4], wi[4], xr[4], xi[4];
+          tw_n1(nt, t1, sc2, wr, wi);
+          twiddle(er, ei, wr, wi, xr, xi);
+          pack_operand<SE != 0>(xr, xi, e[nt][t1][0], e[nt][t1][SE]);
+        }
+      }
+      // inverse over k1 and the last twiddle
+      debug_lds_fence();  // the row's reads (stage over n1) before its write-back below
+#pragma unroll
+      for (int nt = 0; nt < T2; nt++) {
+#pragma unroll
+        for (int mt = 0; mt < T1; mt++) {
+          f4 zr = {0.f, 0.f, 0.f, 0.f}, zi = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int ks = 0; ks < T1; ks++)
+#pragma unroll
+            for (int p = 0; p <= SE; p++) {
+              zr = mfma(f1(mt, ks, 0), e[nt][ks][p], zr);
+              zi = mfma(f1(mt, ks, 1), e[nt][ks][p], zi);
+            }
+          zr = round_acc(zr, acc16);
+          zi = round_acc(zi, acc16);
+          // lane value v is n1 = 16mt + 4g + v, n2 = 16nt + c: m = n1 R2 + n2
+          float wr[4], wi[4], xr[4], xi[4];
+          if constexpr (REC) {
+#pragma unroll
+            for (int v = 0; v < 4; v++) wr[v] = lr[v], wi[v] = li[v];
+            if (i + 1 < ROWS) cmul4(lr, li, fr, fi);
+          } else {
+            twiddle4e<N>(k0 * ((16 * mt + 4 * g) * R2 + 16 * nt + c), k0 * R2, sc1, wr, wi);
+          }
+          twiddle(zr, zi, wr, wi, xr, xi);
+          // back into the row's own block, [n2][n1]: only this wavefront reads the row,
+          // and all of its input is in registers by now
+          const int pos = rb + (16 * nt + c) * P::PA + 16 * mt + 4 * g;
+          *reinterpret_cast<h4*>(re + pos) = to_h4(xr);
+          *reinterpret_cast<h4*>(im + pos) = to_h4(xi);
+        }
       }
     }
-    // inverse over k1 and the last twiddle
-    debug_lds_fence();  // the row's reads (stage over n1) before its write-back below
+  } else {
+    // Rows are taken RP at a time: the operand reads of all of a step's rows come before any
+    // of their write-backs, so the compiler can interleave the rows' independent chains (one
+    // row's write-back to LDS would otherwise order it before the next row's reads, as it
+    // cannot tell the rows' swizzled addresses apart). Each row's arithmetic is the same for
+    // any RP, and the last twiddles step from row to row in the same order.
+    constexpr int RP = RPK;
 #pragma unroll
-    for (int nt = 0; nt < T2; nt++) {
+    for (int i0 = 0; i0 < ROWS; i0 += RP) {
+      int k0[RP], rb[RP];
 #pragma unroll
-      for (int mt = 0; mt < T1; mt++) {
-        f4 zr = {0.f, 0.f, 0.f, 0.f}, zi = {0.f, 0.f, 0.f, 0.f};
+      for (int u = 0; u < RP; u++) {
+        k0[u] = wave * ROWS + i0 + u;  // each wavefront owns ROWS consecutive rows
+        rb[u] = k0[u] * P::ROW;
+      }
 #pragma unroll
-        for (int ks = 0; ks < T1; ks++)
+      for (int u = 0; u < RP; u++) load_row_spectrum(k0[u], kq[u]);  // the step's rows' spectra
+      // stage over n1: A[n2][n1] from the row's [n2 ^ (k0 & 15)][n1] block
+      h8 b[RP][T1][T2][1 + SB];  // [row][k1 tile][n2 tile][hi, lo]: B operands of the stage over n2
+      {
+        h8 a[RP][T2][T1];
 #pragma unroll
-          for (int p = 0; p <= SE; p++) {
-            zr = mfma(f1(mt, ks, 0), e[nt][ks][p], zr);
-            zi = mfma(f1(mt, ks, 1), e[nt][ks][p], zi);
+        for (int u = 0; u < RP; u++)
+#pragma unroll
+          for (int t2 = 0; t2 < T2; t2++)
+#pragma unroll
+            for (int ks = 0; ks < T1; ks++)
+              a[u][t2][ks] = lds_frag(re, im, rb[u] + (16 * t2 + (c ^ (k0[u] & 15))) * P::PA + 16 * ks + 4 * g);
+#pragma unroll
+        for (int t2 = 0; t2 < T2; t2++) {
+#pragma unroll
+          for (int nt = 0; nt < T1; nt++) {
+#pragma unroll
+            for (int u = 0; u < RP; u++) {
+              f4 dr = {0.f, 0.f, 0.f, 0.f}, di = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+              for (int ks = 0; ks < T1; ks++) {
+                dr = mfma(a[u][t2][ks], f1(nt, ks, 0), dr);
+                di = mfma(a[u][t2][ks], f1(nt, ks, 1), di);
+              }
+              dr = round_acc(dr, acc16);
+              di = round_acc(di, acc16);
+              float wr[4], wi[4], xr[4], xi[4];
+              tw_n1(nt, t2, sc1, wr, wi);
+              twiddle(dr, di, wr, wi, xr, xi);
+              pack_operand<SB != 0>(xr, xi, b[u][nt][t2][0], b[u][nt][t2][SB]);
+            }
           }
-        zr = round_acc(zr, acc16);
-        zi = round_acc(zi, acc16);
-        // lane value v is n1 = 16mt + 4g + v, n2 = 16nt + c: m = n1 R2 + n2
-        float wr[4], wi[4], xr[4], xi[4];
-        if constexpr (REC) {
-#pragma unroll
-          for (int v = 0; v < 4; v++) wr[v] = lr[v], wi[v] = li[v];
-          if (i + 1 < ROWS) cmul4(lr, li, fr, fi);
-        } else {
-          twiddle4e<N>(k0 * ((16 * mt + 4 * g) * R2 + 16 * nt + c), k0 * R2, sc1, wr, wi);
         }
-        twiddle(zr, zi, wr, wi, xr, xi);
-        // back into the row's own block, [n2][n1]: only this wavefront reads the row,
-        // and all of its input is in registers by now
-        const int pos = rb + (16 * nt + c) * P::PA + 16 * mt + 4 * g;
-        *reinterpret_cast<h4*>(re + pos) = to_h4(xr);
-        *reinterpret_cast<h4*>(im + pos) = to_h4(xi);
+      }
+      // stage over n2, spectrum, inverse over k2
+      h8 e[RP][T2][T1][1 + SE];  // [row][n2 tile][k1 tile][hi, lo]: B operands of the inverse over k1
+#pragma unroll
+      for (int t1 = 0; t1 < T1; t1++) {
+#pragma unroll
+        for (int u = 0; u < RP; u++) {
+          f4 dr[T2], di[T2];
+#pragma unroll
+          for (int mt = 0; mt < T2; mt++) {
+            dr[mt] = (f4){0.f, 0.f, 0.f, 0.f};
+            di[mt] = (f4){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int ks = 0; ks < T2; ks++)
+#pragma unroll
+              for (int p = 0; p <= SB; p++) {
+                dr[mt] = mfma(f2(mt, ks, 0), b[u][t1][ks][p], dr[mt]);
+                di[mt] = mfma(f2(mt, ks, 1), b[u][t1][ks][p], di[mt]);
+              }
+            dr[mt] = round_acc(dr[mt], acc16);
+            di[mt] = round_acc(di[mt], acc16);
+          }
+          h8 a2[T2], a2lo[SA ? T2 : 1];
+          spectrum_product<T2, SA>(dr, di, kq[u][t1], a2, a2lo);
+#pragma unroll
+          for (int nt = 0; nt < T2; nt++) {
+            f4 er = {0.f, 0.f, 0.f, 0.f}, ei = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int mt = 0; mt < T2; mt++) {
+              er = mfma(a2[mt], f2(nt, mt, 0), er);
+              ei = mfma(a2[mt], f2(nt, mt, 1), ei);
+              if constexpr (SA) {
+                er = mfma(a2lo[mt], f2(nt, mt, 0), er);
+                ei = mfma(a2lo[mt], f2(nt, mt, 1), ei);
+              }
+            }
+            er = round_acc(er, acc16);
+            ei = round_acc(ei, acc16);
+            float wr[4], wi[4], xr[4], xi[4];
+            tw_n1(nt, t1, sc2, wr, wi);
+            twiddle(er, ei, wr, wi, xr, xi);
+            pack_operand<SE != 0>(xr, xi, e[u][nt][t1][0], e[u][nt][t1][SE]);
+          }
+        }
+      }
+      // inverse over k1 and the last twiddle
+      debug_lds_fence();  // the rows' reads (stage over n1) before their write-back below
+#pragma unroll
+      for (int u = 0; u < RP; u++) {
+#pragma unroll
+        for (int nt = 0; nt < T2; nt++) {
+#pragma unroll
+          for (int mt = 0; mt < T1; mt++) {
+            f4 zr = {0.f, 0.f, 0.f, 0.f}, zi = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int ks = 0; ks < T1; ks++)
+#pragma unroll
+              for (int p = 0; p <= SE; p++) {
+                zr = mfma(f1(mt, ks, 0), e[u][nt][ks][p], zr);
+                zi = mfma(f1(mt, ks, 1), e[u][nt][ks][p], zi);
+              }
+            zr = round_acc(zr, acc16);
+            zi = round_acc(zi, acc16);
+            // lane value v is n1 = 16mt + 4g + v, n2 = 16nt + c: m = n1 R2 + n2
+            float wr[4], wi[4], xr[4], xi[4];
+            if constexpr (REC) {
+#pragma unroll
+              for (int v = 0; v < 4; v++) wr[v] = lr[v], wi[v] = li[v];
+              if (i0 + u + 1 < ROWS) cmul4(lr, li, fr, fi);
+            } else {
+              twiddle4e<N>(k0[u] * ((16 * mt + 4 * g) * R2 + 16 * nt + c), k0[u] * R2, sc1, wr, wi);
+            }
+            twiddle(zr, zi, wr, wi, xr, xi);
+            // back into the row's own block, [n2][n1]: only this wavefront reads the row,
+            // and all of its input is in registers by now
+            const int pos = rb[u] + (16 * nt + c) * P::PA + 16 * mt + 4 * g;
+            *reinterpret_cast<h4*>(re + pos) = to_h4(xr);
+            *reinterpret_cast<h4*>(im + pos) = to_h4(xi);
+          }
+        }
       }
     }
   }
