@@ -311,7 +311,7 @@ def sweep(a, sf, torch, np, dev, cover):
             plan = sf.default_plan(L, io, B)
             sets, _, set_bytes = make_workload(sf, torch, dev, B, H, L, io, plan, a.rotate_mb)
             ms, _, ms_warm, exact, step = time_fused(sf, torch, cover, sets, plan, a.steps, 3, warm=True,
-                                                     gpu_warm_ms=min(a.gpu_warm_ms, 50.0))
+                                                     gpu_warm_ms=a.gpu_warm_ms)
             ms_ref = reference_protocol_ms(cover, lambda: step(0), L)
             s_io = 4 if io == "fp32" else 2
             algo = B * H * L * 2 * s_io + H * 2 * L * 8
