@@ -55,7 +55,7 @@
 
 // k0 rows per phase-2 step of three-stage plans (each wavefront's rows taken this many at a time)
 #ifndef SFFFT_WG_ROWS
-#define SFFFT_WG_ROWS 2
+#define SFFFT_WG_ROWS 4
 #endif
 
 namespace sffft {
@@ -671,7 +671,10 @@ __device__ __forceinline__ void phase2_s3(_Float16* re, _Float16* im, const floa
   // rows per step (RP below): plans with one 16x16 tile per row only; with more tiles per
   // row, two rows at a time took more VGPRs than the occupancy allows (L = 8192: 13-15%
   // slower) or gained nothing (L = 16384: 2% slower)
-  constexpr int RPK = T1 * T2 == 1 && ROWS % SFFFT_WG_ROWS == 0 ? SFFFT_WG_ROWS : 1;
+  constexpr int RPK = T1 * T2 != 1              ? 1
+                      : ROWS % SFFFT_WG_ROWS == 0 ? SFFFT_WG_ROWS
+                      : ROWS % 2 == 0             ? 2
+                                                  : 1;
   float4 kq[RPK > 1 ? RPK : KQB][T1][T2][2];
   auto load_row_spectrum = [&](int k0, float4 (*q)[T2][2]) {
 #pragma unroll
