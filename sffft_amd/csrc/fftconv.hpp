@@ -695,6 +695,9 @@ __device__ __forceinline__ void phase2_s3(_Float16* re, _Float16* im, const floa
     twiddle4e<N>(wave * ROWS * m0, wave * ROWS * R2, sc1, lr, li);
     twiddle4e<N>(m0, R2, 1.f, fr, fi);
   }
+  // Two forms of the same row loop. One row per step keeps the loop that the multi-tile
+  // plans were tuned with: the several-row form, even with one row per step, changes how
+  // the compiler schedules and allocates them (up to 5 more spills in some variants).
   if constexpr (RPK == 1) {
 #pragma unroll
     for (int i = 0; i < ROWS; i++) {
