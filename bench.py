@@ -51,6 +51,11 @@ def parse():
     ap.add_argument("--mode", type=int, default=None, help="0: workgroup per transform, 1: wavefront per pair")
     ap.add_argument("--channels", type=int, default=None, help="mode 1: channels per workgroup")
     ap.add_argument("--acc", type=int, default=0)
+    ap.add_argument("--repeats", type=int, default=5,
+                    help="timed replays of the K-step graph per measurement; ms is their median")
+    ap.add_argument("--configs", type=int, default=1,
+                    help="also time the other benchmark configurations (the `configs` key): L=2048 bf16 "
+                         "16x16x16 with fp32 and fp16 accumulation, and B=4 H=1536 L=16384 bf16")
     ap.add_argument("--gpu-warm-ms", type=float, default=300.0,
                     help="before the timed steps, replay the captured steps for about this long so the GPU "
                          "runs at its steady clocks (untimed)")
@@ -111,6 +116,107 @@ class Cover:
 
     def __call__(self, ms: float) -> None:
         self.torch.cuda._sleep(int(self.cycles_per_ms * ms))
+
+
+class Clocks:
+    """GFX clock (SCLK), memory clock (MCLK), socket power, hotspot temperature and GFX
+    activity of the GPU behind cuda:0, read through amdsmi (matched by PCI address), so that
+    timings taken on different boxes or at different points of one run can be told apart.
+    start() begins sampling every couple of milliseconds on a host thread, stop() returns the
+    median, min and max of each field over the samples. Reading only; an "error" entry where
+    the library or the device is unavailable."""
+
+    FIELDS = (("sclk_mhz", ("current_gfxclk", "current_gfxclks", "average_gfxclk_frequency")),
+              ("mclk_mhz", ("current_uclk", "average_uclk_frequency")),
+              ("power_w", ("current_socket_power", "average_socket_power")),
+              ("hotspot_c", ("temperature_hotspot",)),
+              ("gfx_activity_pct", ("average_gfx_activity",)))
+
+    def __init__(self, period_s=0.002):
+        self.h, self.error, self.period = None, None, period_s
+        self._thread, self._samples = None, []
+        try:
+            import amdsmi
+            import torch
+
+            self.amdsmi = amdsmi
+            amdsmi.amdsmi_init()
+            p = torch.cuda.get_device_properties(0)
+            want = f"{p.pci_domain_id:04x}:{p.pci_bus_id:02x}:{p.pci_device_id:02x}"
+            handles = amdsmi.amdsmi_get_processor_handles()
+            for h in handles:
+                if amdsmi.amdsmi_get_gpu_device_bdf(h).lower().startswith(want):
+                    self.h = h
+            if self.h is None and len(handles) == 1:
+                self.h = handles[0]
+            if self.h is None:
+                self.error = f"no amdsmi device at {want}"
+        except Exception as e:  # noqa: BLE001  (reported, never fatal)
+            self.error = f"{type(e).__name__}: {e}"
+
+    @staticmethod
+    def _num(v):
+        if isinstance(v, (list, tuple)):
+            vals = [x for x in v if isinstance(x, (int, float)) and 0 < x < 1 << 31]
+            return round(sum(vals) / len(vals), 1) if vals else None
+        return v if isinstance(v, (int, float)) and 0 <= v < 1 << 31 else None
+
+    def read(self):
+        """One sample: {field: value or None}, or {"error": ...}."""
+        if self.h is None:
+            return {"error": self.error}
+        try:
+            m = self.amdsmi.amdsmi_get_gpu_metrics_info(self.h)
+        except Exception as e:  # noqa: BLE001
+            return {"error": f"{type(e).__name__}: {e}"}
+        out = {}
+        for key, names in self.FIELDS:
+            out[key] = None
+            for n in names:
+                v = self._num(m.get(n))
+                if v is not None:
+                    out[key] = v
+                    break
+        return out
+
+    def start(self):
+        import threading
+
+        self._samples = []
+        if self.h is None:
+            return
+        self._stop = threading.Event()
+
+        def run():
+            while not self._stop.is_set():
+                self._samples.append(self.read())
+                self._stop.wait(self.period)
+
+        self._thread = threading.Thread(target=run, daemon=True)
+        self._thread.start()
+
+    def stop(self):
+        import statistics
+
+        if self._thread is None:
+            return {"error": self.error}
+        self._stop.set()
+        self._thread.join()
+        self._thread = None
+        good = [x for x in self._samples if "error" not in x]
+        out = {"samples": len(good)}
+        for key, _ in self.FIELDS:
+            vals = [x[key] for x in good if x.get(key) is not None]
+            out[key] = ({"median": statistics.median(vals), "min": min(vals), "max": max(vals)} if vals else None)
+        return out
+
+
+def clock_brief(c):
+    """Median SCLK/MCLK/power of a Clocks.stop() summary, for the progress lines."""
+    if not c or "error" in c:
+        return c
+    med = lambda k: None if c.get(k) is None else c[k]["median"]  # noqa: E731
+    return f"sclk {med('sclk_mhz')} MHz mclk {med('mclk_mhz')} MHz {med('power_w')} W ({c['samples']} samples)"
 
 
 def events_ms(cover, fn, reps, host_ms):
@@ -177,8 +283,27 @@ def copy_reference(a):
                       "frac_of_8TBps": round(gbs / HBM_PEAK_GBS, 4)}), flush=True)
 
 
-def make_workload(sf, torch, dev, B, H, L, io, plan, rotate_mb, seed=0):
-    """Rotated (u, spectrum, y) buffer sets of the benchmark workload, synthetic, in HBM."""
+def sinusoid_filters(torch, dev, H, L, g):
+    """Hyena-style long filters: k[h, n] = sum_{i<16} A_hi sin(w_hi n) exp(-a_h n) with
+    w ~ U(0, pi), A ~ N(0, 1) and a_h log-uniform in [1e-4, 1e-2], evaluated in float64 on
+    the device (128 channels at a time), returned as float32."""
+    import math
+
+    w = torch.rand(H, 16, device=dev, dtype=torch.float64, generator=g) * math.pi
+    amp = torch.randn(H, 16, device=dev, dtype=torch.float64, generator=g)
+    lo, hi = math.log(1e-4), math.log(1e-2)
+    alpha = torch.exp(lo + (hi - lo) * torch.rand(H, device=dev, dtype=torch.float64, generator=g))
+    n = torch.arange(L, device=dev, dtype=torch.float64)
+    k = torch.empty(H, L, device=dev, dtype=torch.float64)
+    for h in range(0, H, 128):
+        s = slice(h, h + 128)
+        k[s] = (amp[s, :, None] * torch.sin(w[s, :, None] * n)).sum(1) * torch.exp(-alpha[s, None] * n)
+    return k.float()
+
+
+def make_workload(sf, torch, dev, B, H, L, io, plan, rotate_mb, seed=0, filters="decay"):
+    """Rotated (u, spectrum, y) buffer sets of the benchmark workload, synthetic, in HBM.
+    filters: "decay" (k ~ N(0,1) exp(-n/decay)/sqrt(L)) or "sines" (sinusoid_filters)."""
     import numpy as np
 
     g = torch.Generator(device=dev).manual_seed(seed)
@@ -190,7 +315,10 @@ def make_workload(sf, torch, dev, B, H, L, io, plan, rotate_mb, seed=0):
     nsets = 1 if rotate_mb <= 0 or set_bytes > rotate_mb * 1e6 else max(3, int(np.ceil(rotate_mb * 1e6 / set_bytes)))
     sets = []
     for i in range(nsets):
-        k = torch.randn(H, L, device=dev, generator=g) * torch.exp(-n / decay) / L ** 0.5
+        if filters == "sines":
+            k = sinusoid_filters(torch, dev, H, L, g)
+        else:
+            k = torch.randn(H, L, device=dev, generator=g) * torch.exp(-n / decay) / L ** 0.5
         u32 = torch.randn(B, H, L, device=dev, generator=g)
         u = sf.to_bf16(u32) if io == "bf16" else u32
         kf = sf.spectrum(k, L, plan)
@@ -199,11 +327,16 @@ def make_workload(sf, torch, dev, B, H, L, io, plan, rotate_mb, seed=0):
     return sets, decay, set_bytes
 
 
-def time_fused(sf, torch, cover, sets, plan, steps, warmup, work=None, warm=True, gpu_warm_ms=0.0):
-    """ms per step of K graph-replayed steps over the rotated sets; also the same steps
-    launched eagerly, the warm single-set time, and whether the replay reproduced the
-    eager outputs bit for bit. Before the timed replay the captured steps are replayed,
-    untimed, for about gpu_warm_ms, so the GPU leaves its idle clocks first."""
+def time_fused(sf, torch, cover, sets, plan, steps, warmup, work=None, warm=True, gpu_warm_ms=0.0, repeats=5,
+               clocks=None):
+    """K graph-replayed steps over the rotated sets, timed `repeats` times: ms per step as the
+    median of the replays, with their min, max and every value; the GPU clocks before and
+    after the timed replays; the same steps launched eagerly; the warm single-set time (median
+    of as many replays); and whether the replays reproduced the eager outputs bit for bit.
+    Before the timed replays the captured steps are replayed, untimed, for about gpu_warm_ms,
+    so the GPU leaves its idle clocks first."""
+    import statistics
+
     nsets = len(sets)
 
     def step(i):
@@ -221,13 +354,16 @@ def time_fused(sf, torch, cover, sets, plan, steps, warmup, work=None, warm=True
         for i in range(steps):
             step(i)
     graph.replay()  # untimed replay
+    if clocks:  # sampled through the untimed and the timed replays
+        clocks.start()
     t_warm = time.perf_counter()
     while (time.perf_counter() - t_warm) * 1e3 < gpu_warm_ms:
         graph.replay()
         torch.cuda.synchronize()
     host = host_time_ms(graph.replay)
     exact = all(torch.equal(s["y"], y0) for s, y0 in zip(sets, y_eager))
-    ms = events_ms(cover, graph.replay, steps, host)
+    runs = [events_ms(cover, graph.replay, steps, host) for _ in range(max(1, repeats))]
+    clk = clocks.stop() if clocks else None
     exact = exact and all(torch.equal(s["y"], y0) for s, y0 in zip(sets, y_eager))
     eager = lambda: [step(i) for i in range(steps)]  # noqa: E731
     ms_eager = events_ms(cover, eager, steps, host_time_ms(eager))
@@ -239,10 +375,14 @@ def time_fused(sf, torch, cover, sets, plan, steps, warmup, work=None, warm=True
             for i in range(steps):
                 step(0)
         warm_graph.replay()
-        ms_warm = events_ms(cover, warm_graph.replay, steps, host_time_ms(warm_graph.replay))
+        host_w = host_time_ms(warm_graph.replay)
+        ms_warm = statistics.median(events_ms(cover, warm_graph.replay, steps, host_w)
+                                    for _ in range(max(1, repeats)))
         del warm_graph
     del graph
-    return ms, ms_eager, ms_warm, exact, step
+    return {"ms": statistics.median(runs), "ms_min": min(runs), "ms_max": max(runs), "ms_runs": runs,
+            "ms_eager": ms_eager, "ms_warm": ms_warm, "exact": exact, "step": step,
+            "clocks": clk}
 
 
 def all_output_error(oracle, np, sets, B, H, L, y=None):
@@ -294,7 +434,7 @@ def cpu_baseline(oracle, np, u_np, k_np, B, H, L, seconds, cores):
     return {"value": round(value, 3), "unit": "ms per batch", "cores": cores, "kind": "port", "sample": sample}
 
 
-def sweep(a, sf, torch, np, dev, cover):
+def sweep(a, sf, torch, np, dev, cover, clocks):
     """Every L of the reference table in fp32 and bf16 I/O (src/sffft.cu:506-513,
     README.md:27-35): graph-timed rotated ms, roofline fraction, all-output rel-L2
     against fp64, and the reference's own warm protocol for the fused launch and the
@@ -310,8 +450,9 @@ def sweep(a, sf, torch, np, dev, cover):
             t0 = time.perf_counter()
             plan = sf.default_plan(L, io, B)
             sets, _, set_bytes = make_workload(sf, torch, dev, B, H, L, io, plan, a.rotate_mb)
-            ms, _, ms_warm, exact, step = time_fused(sf, torch, cover, sets, plan, a.steps, 3, warm=True,
-                                                     gpu_warm_ms=a.gpu_warm_ms)
+            t = time_fused(sf, torch, cover, sets, plan, a.steps, 3, warm=True, gpu_warm_ms=a.gpu_warm_ms,
+                           repeats=a.repeats, clocks=clocks)
+            ms, ms_warm, exact, step = t["ms"], t["ms_warm"], t["exact"], t["step"]
             ms_ref = reference_protocol_ms(cover, lambda: step(0), L)
             s_io = 4 if io == "fp32" else 2
             algo = B * H * L * 2 * s_io + H * 2 * L * 8
@@ -332,7 +473,8 @@ def sweep(a, sf, torch, np, dev, cover):
                 rp.close()
                 del yr
             row = {"L": L, "io": io, "plan": plan.name(), "waves": plan.waves, "mode": plan.mode,
-                   "channels": plan.channels, "ms": round(ms, 6), "ms_warm": round(ms_warm, 6),
+                   "channels": plan.channels, "ms": round(ms, 6), "ms_min": round(t["ms_min"], 6),
+                   "ms_max": round(t["ms_max"], 6), "ms_warm": round(ms_warm, 6), "clocks": t["clocks"],
                    "roofline_frac": round(algo / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
                    "rel_l2_vs_fp64": err, "ms_reference_protocol": round(ms_ref, 6),
                    "rocfft_pipeline_ms": None if rocfft_ms is None else round(rocfft_ms, 6),
@@ -343,8 +485,10 @@ def sweep(a, sf, torch, np, dev, cover):
             if xcheck is not None:
                 row["oracle_fft_vs_direct"] = xcheck
             rows.append(row)
-            print(f"# sweep L={L} {io} {plan.name()}: {ms * 1e3:.2f} us frac {row['roofline_frac']} "
-                  f"err {err:.3e} rocfft {rocfft_ms} ({time.perf_counter() - t0:.1f} s)", file=sys.stderr, flush=True)
+            print(f"# sweep L={L} {io} {plan.name()}: {ms * 1e3:.2f} us (min {t['ms_min'] * 1e3:.2f} max "
+                  f"{t['ms_max'] * 1e3:.2f}) frac {row['roofline_frac']} err {err:.3e} rocfft {rocfft_ms} "
+                  f"clocks {clock_brief(t['clocks'])} ({time.perf_counter() - t0:.1f} s)", file=sys.stderr,
+                  flush=True)
             del sets
             torch.cuda.empty_cache()
     # the fp32 rocFFT pipeline is the comparator of both I/O rows of a length
@@ -353,6 +497,56 @@ def sweep(a, sf, torch, np, dev, cover):
         if r["io"] == "bf16":
             f = by_L[r["L"]]
             r["speedup_vs_rocfft"] = round(f["rocfft_pipeline_ms"] / r["ms_reference_protocol"], 2)
+    return rows
+
+
+# The benchmark configurations beside the headline and the sweep: (name, B, H, L, io, plan
+# spec, waves, seqs, mode, channels, acc, filters); plan None = the tuned default.
+CONFIG_ROWS = (
+    ("L=2048 bf16 16x16x16, fp32 accumulation", 8, 768, 2048, "bf16", "16x16x16", 4, 2, 0, 1, 0, "decay"),
+    ("L=2048 bf16 16x16x16, fp16 accumulation", 8, 768, 2048, "bf16", "16x16x16", 4, 2, 0, 1, 1, "decay"),
+    ("Hyena-style long filter B=4 H=1536 L=16384 bf16", 4, 1536, 16384, "bf16", None, 0, 0, 0, 0, 0, "sines"),
+)
+
+
+def config_rows(a, sf, torch, np, dev, cover, clocks):
+    """The other benchmark configurations (CONFIG_ROWS), each timed like the sweep rows
+    (median of the graph replays over rotated sets, warm time, the reference protocol)
+    with its all-output error against the fp64 oracle."""
+    import oracle
+
+    rows = []
+    for name, B, H, L, io, spec, waves, seqs, mode, channels, acc, filters in CONFIG_ROWS:
+        t0 = time.perf_counter()
+        if spec is None:
+            plan = sf.default_plan(L, io, B, acc=acc)
+        else:
+            plan = sf.make_plan(spec, waves, acc=acc, cached=1, seqs=seqs, mode=mode, channels=channels)
+        sets, _, set_bytes = make_workload(sf, torch, dev, B, H, L, io, plan, a.rotate_mb, filters=filters)
+        t = time_fused(sf, torch, cover, sets, plan, a.steps, 3, warm=True, gpu_warm_ms=a.gpu_warm_ms,
+                       repeats=a.repeats, clocks=clocks)
+        ms_ref = reference_protocol_ms(cover, lambda: t["step"](0), L)
+        ref, xcheck = all_output_error(oracle, np, sets, B, H, L)
+        t["step"](0)
+        torch.cuda.synchronize()
+        err = oracle.rel_l2(sets[0]["y"].float().cpu().numpy(), ref)
+        del ref
+        s_io = 4 if io == "fp32" else 2
+        algo = B * H * L * 2 * s_io + H * 2 * L * 8
+        row = {"config": name, "B": B, "H": H, "L": L, "io": io, "plan": plan.name(), "waves": plan.waves,
+               "seqs": plan.seqs, "mode": plan.mode, "channels": plan.channels,
+               "acc": "fp16" if plan.acc else "fp32", "filters": filters, "ms": round(t["ms"], 6),
+               "ms_min": round(t["ms_min"], 6), "ms_max": round(t["ms_max"], 6), "ms_warm": round(t["ms_warm"], 6),
+               "ms_reference_protocol": round(ms_ref, 6),
+               "roofline_frac": round(algo / (t["ms"] * 1e-3) / 1e9 / HBM_PEAK_GBS, 4), "rel_l2_vs_fp64": err,
+               "oracle_fft_vs_direct": xcheck, "graph_replay_bitexact": bool(t["exact"]),
+               "rotated_sets": len(sets), "clocks": t["clocks"]}
+        rows.append(row)
+        print(f"# config {name} {plan.name()} w{plan.waves}: {t['ms'] * 1e3:.2f} us (min {t['ms_min'] * 1e3:.2f} "
+              f"max {t['ms_max'] * 1e3:.2f}) frac {row['roofline_frac']} err {err:.3e} "
+              f"clocks {clock_brief(t['clocks'])} ({time.perf_counter() - t0:.1f} s)", file=sys.stderr, flush=True)
+        del sets
+        torch.cuda.empty_cache()
     return rows
 
 
@@ -394,6 +588,7 @@ def main():
 
     t_start = time.perf_counter()
     cover = Cover()
+    clocks = Clocks()
     # ---- synthetic inputs (the benchmark workload), resident in HBM -------------
     sets, decay, set_bytes = make_workload(sf, torch, dev, B, H, L, io, plan, a.rotate_mb)
     s_io = 4 if io == "fp32" else 2
@@ -409,8 +604,10 @@ def main():
     # graph is replayed between two events on the replay stream, behind a spin kernel
     # that covers the host's enqueue time. The same K steps launched eagerly are timed
     # beside it, and the same K steps on one buffer set (warm).
-    ms, ms_eager, ms_warm, replay_exact, step = time_fused(sf, torch, cover, sets, plan, a.steps, a.warmup, work,
-                                                           gpu_warm_ms=a.gpu_warm_ms)
+    timed = time_fused(sf, torch, cover, sets, plan, a.steps, a.warmup, work, gpu_warm_ms=a.gpu_warm_ms,
+                       repeats=a.repeats, clocks=clocks)
+    ms, ms_eager, ms_warm, replay_exact, step = (timed["ms"], timed["ms_eager"], timed["ms_warm"], timed["exact"],
+                                                 timed["step"])
 
     # dispatch floor: a body-less kernel with the same grid, block and LDS size, K
     # launches replayed as a graph like the convolution (first call eager: it sets the
@@ -452,7 +649,8 @@ def main():
     del sets, work
     torch.cuda.empty_cache()
 
-    rows = sweep(a, sf, torch, np, dev, cover) if a.sweep and plan.mode != 2 else None
+    rows = sweep(a, sf, torch, np, dev, cover, clocks) if a.sweep and plan.mode != 2 else None
+    cfg_rows = config_rows(a, sf, torch, np, dev, cover, clocks) if a.configs and plan.mode != 2 else None
 
     # ---- CPU baseline: the reference's fp64 direct convolution (oracle port) ----
     # A bounded sample of the same workload on all host threads, and on one thread.
@@ -490,13 +688,19 @@ def main():
                      "traffic": profiled_traffic(f"B={B} H={H} L={L} {io}", plan, stamp)},
         "cpu_baseline": cpu,
         "cpu_baseline_1core": cpu1,
+        "ms_min": round(timed["ms_min"], 6),
+        "ms_max": round(timed["ms_max"], 6),
+        "ms_runs": [round(x, 6) for x in timed["ms_runs"]],
+        "repeats": a.repeats,
+        "clocks": timed["clocks"],
         "ms_warm": round(ms_warm, 6),
         "ms_eager": round(ms_eager, 6),
         "ms_dispatch_floor": None if ms_floor is None else round(ms_floor, 6),
         "io_only_frac": round(B * H * L * 2 * s_io / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
         "timing": ("HIP graph of the K steps replayed between events behind a spin kernel that covers the "
-                   "host enqueue, after W eager warmup steps and untimed replays for gpu_warm_ms; ms_eager: the "
-                   "same steps launched one by one"),
+                   "host enqueue, after W eager warmup steps and untimed replays for gpu_warm_ms; value: the median "
+                   "ms per step of `repeats` such replays (ms_min, ms_max, ms_runs); clocks: amdsmi samples every "
+                   "2 ms through the untimed and timed replays; ms_eager: the same steps launched one by one"),
         "gpu_warm_ms": a.gpu_warm_ms,
         "graph_replay_bitexact": bool(replay_exact),
         "rel_l2_vs_fp64": rel_err,
@@ -505,6 +709,7 @@ def main():
         "algorithmic_bytes": algo_bytes,
         "kernel_sources_sha": stamp,
         "sweep": rows,
+        "configs": cfg_rows,
         "wall_s": round(time.perf_counter() - t_start, 1),
     }
     print(json.dumps(out), flush=True)

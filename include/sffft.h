@@ -85,11 +85,13 @@ int sffft_plan_get(int L, int index, sffft_plan* plan, char* name, size_t name_l
 /* Bytes of the kernel-order filter spectrum: H * 2L * 8 (complex64). */
 size_t sffft_spectrum_bytes(int H, int L);
 
-/* Filter spectrum in the fused kernel's order, from the real filter k [H][L] fp32.
- * The order depends on the radices and on the mode (mode 0 and mode 1 differ). For mode-1
- * (wave) plans only the Hermitian half is stored (K[2L-f] = conj(K[f]) for a real filter):
- * (r0/2 + 1) * (8*(r1/16) + 1) * 2 complex64 values per channel, channels consecutive, at
- * the start of kf; the rest of the sffft_spectrum_bytes buffer is zeroed.
+/* Filter spectrum in the fused kernel's order, from the real filter k [H][L] fp32, as
+ * kf [H][2L] complex64: row h holds channel h's spectrum for every plan, so rows of
+ * spectra may be sliced and concatenated along the channels. The order within a row
+ * depends on the radices and on the mode (mode 0 and mode 1 differ). For mode-1 (wave)
+ * plans only the Hermitian half is stored (K[2L-f] = conj(K[f]) for a real filter):
+ * (r0/2 + 1) * (8*(r1/16) + 1) * 2 complex64 values at the start of each row, the rest of
+ * the row zero.
  * `work` must hold sffft_spectrum_bytes(H, L) bytes (scratch, clobbered).
  * Replaces: zero-pad + cufftExecC2C(FORWARD) + permuteK (src/sffft.cu:342-344,365,384,283-288).
  * Arithmetic: fp64 accumulation and twiddles, fp32 storage between the stages. */
@@ -122,10 +124,19 @@ int sffft_spectrum_noalloc(const float* k, int H, int L, const sffft_plan* plan,
 int sffft_spectrum_complex(const float* kr, const float* ki, int H, int L, const sffft_plan* plan, void* kf,
                            void* work, void* stream);
 
-/* Same, from an unnormalised natural-order spectrum kc [H][2L] complex64
- * (kc[h][f] = sum_n k[h][n] exp(-2 pi i f n / 2L), e.g. from hipFFT C2C).
+/* sffft_spectrum from an unnormalised natural-order spectrum kc [H][2L] complex64
+ * (kc[h][f] = sum_n k[h][n] exp(-2 pi i f n / 2L), e.g. from hipFFT C2C) of a REAL filter k:
+ * for mode-1 plans only the Hermitian half of kc is read (frequencies above L are taken as
+ * the conjugates of their partners 2L - f), so kc must be the spectrum of a real filter.
  * Replaces permuteK (src/sffft.cu:283-288). kc and kf must not overlap. */
 int sffft_spectrum_from_natural(const void* kc, int H, int L, const sffft_plan* plan, void* kf, void* stream);
+
+/* The same gather for any spectrum kc, e.g. of a complex filter kr + i*ki: every frequency
+ * is read and the whole spectrum stored, the layout sffft_spectrum_complex writes, for
+ * sffft_conv_complex_* (and sffft_conv_long_*). Plans with two sequences per transform
+ * (seqs = 2). No counterpart in the reference (real filters only, README.md:174). */
+int sffft_spectrum_from_natural_complex(const void* kc, int H, int L, const sffft_plan* plan, void* kf,
+                                        void* stream);
 
 /* The fused convolution, one launch: grid = H*B/seqs workgroups of 64*waves lanes
  * (mode 0) or ceil(H / channels) workgroups of 64*waves lanes (mode 1).
@@ -184,7 +195,10 @@ int sffft_circconv_long_bf16(const uint16_t* u, const void* kf, uint16_t* y, voi
  * with the minus sign for inverse = 0 and the plus sign for inverse = 1. N is a power of two
  * in [2, 2^24] and batch * N <= 2^31. Element n of sequence b sits at x[b * dist + n * stride]
  * (complex elements, stride >= 1, dist >= 1 when batch > 1); X has the same layout and may
- * equal x. `work` holds sffft_fft_work_bytes(batch, N) bytes (NULL allowed when that is 0) and
+ * equal x. Two layout families are supported: whole sequences one after another
+ * (dist >= N * stride) and sequences interleaved within one element step
+ * (stride >= batch * dist, as the columns of a row-major matrix); other layouts, even
+ * non-overlapping ones, are rejected with SFFFT_EINVAL. `work` holds sffft_fft_work_bytes(batch, N) bytes (NULL allowed when that is 0) and
  * must not overlap x or X. Each stage is a radix-<=64 DFT evaluated in fp64 and stored as
  * complex64 (relative error ~1e-7); pointers 8-byte aligned. sffft_fft_work_bytes returns 0
  * for sizes the call rejects. */
@@ -220,6 +234,19 @@ int sffft_dispatch_floor(int B, int H, int L, const sffft_plan* plan, void* stre
 /* Copies the device DFT coefficient table (57,344 bytes) to host memory `out`
  * (for tests). Returns SFFFT_EINVAL if out_len is too small. */
 int sffft_dft_table(void* out, size_t out_len);
+
+/* Test probes of the twiddle factors (no counterpart in the reference; the reference's
+ * twid(), src/sffft.cu:106-113, evaluates them with __sincosf in the kernel).
+ * sffft_twiddle_probe evaluates on the device, with the workgroup kernel's own code
+ * (v_sin/v_cos of the angle in revolutions plus complex recurrences), for each of the nq
+ * queries (e0, step, f0, fstep) (device int[4] each): the four values
+ * sc * exp(-2 pi i (e0 + step*v) / N), v = 0..3, and `rows` (<= 64) row steps, each the
+ * product with exp(-2 pi i (f0 + fstep*v) / N); out is device complex64 [nq][rows+1][4].
+ * N a power of two in [256, 32768]. sffft_twiddle_table copies the wave pipeline's fp32
+ * twiddle tables of plan r0 x r1 (built in fp64 on the host; layout 1 = split, the wave
+ * kernels', 0 = paired, the multi-pass row pass's) to host memory `out`: r0*r1*16 bytes. */
+int sffft_twiddle_probe(int N, const void* queries, int nq, int rows, float sc, void* out, void* stream);
+int sffft_twiddle_table(int r0, int r1, int split, void* out, size_t out_len);
 
 /* Host-side selector (src/selection.h:8-29). A candidate is (method, io, config, ms,
  * rel_err); io is "fp32" or "bf16". Returns the index of the fastest candidate whose io

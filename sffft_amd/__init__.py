@@ -111,6 +111,7 @@ def load_library(path: str) -> ctypes.CDLL:
         "sffft_spectrum": (ci, [vp, ci, ci, P, vp, vp, vp]),
         "sffft_spectrum_conj": (ci, [vp, ci, ci, P, vp, vp, vp]),
         "sffft_spectrum_from_natural": (ci, [vp, ci, ci, P, vp, vp]),
+        "sffft_spectrum_from_natural_complex": (ci, [vp, ci, ci, P, vp, vp]),
         "sffft_spectrum_noalloc": (ci, [vp, ci, ci, P, vp, vp]),
         "sffft_conv_f32": (ci, [vp, vp, vp, ci, ci, ci, P, vp]),
         "sffft_conv_bf16": (ci, [vp, vp, vp, ci, ci, ci, P, vp]),
@@ -133,6 +134,8 @@ def load_library(path: str) -> ctypes.CDLL:
         "sffft_to_bf16": (ci, [vp, vp, sz, vp]),
         "sffft_dispatch_floor": (ci, [ci, ci, ci, P, vp]),
         "sffft_dft_table": (ci, [vp, sz]),
+        "sffft_twiddle_probe": (ci, [ci, vp, ci, ci, ctypes.c_float, vp, vp]),
+        "sffft_twiddle_table": (ci, [ci, ci, ci, vp, sz]),
         "sffft_select_candidate": (ci, [ctypes.POINTER(Candidate), ci, ctypes.c_double, ctypes.c_char_p]),
         "sffft_relative_l2": (ctypes.c_double, [ctypes.c_double, ctypes.c_double]),
         "sffft_strerror": (ctypes.c_char_p, [ci]),
@@ -262,6 +265,17 @@ def _ptr(t) -> ctypes.c_void_p:
     return ctypes.c_void_p(t.data_ptr())
 
 
+def _check_spectrum(kf, u, H: int, N: int) -> None:
+    """kf must be the [H, N] complex64 spectrum buffer of u's H channels (row h is channel h),
+    contiguous and on u's device: the kernels read H rows of N values from its start."""
+    import torch
+
+    if not (kf.is_cuda and kf.dtype == torch.complex64 and kf.is_contiguous() and kf.device == u.device
+            and tuple(kf.shape) == (H, N)):
+        raise ValueError(f"kf must be a contiguous complex64 [H, 2L] = [{H}, {N}] tensor on {u.device} "
+                         f"(a spectrum of this call's channels), got {tuple(kf.shape)} {kf.dtype} on {kf.device}")
+
+
 def spectrum(k, L: int, plan: Plan, work=None, conj: bool = False):
     """Kernel-order filter spectrum [H, 2L] complex64 from the real filter k [H, L] (fp32, cuda);
     with conj, the conjugate spectrum (sffft_spectrum_conj), on which sffft_conv_* computes the
@@ -279,15 +293,17 @@ def spectrum(k, L: int, plan: Plan, work=None, conj: bool = False):
     return kf
 
 
-def spectrum_from_natural(kc, L: int, plan: Plan):
-    """Kernel-order spectrum from the unnormalised natural-order spectrum kc [H, 2L] complex64."""
+def spectrum_from_natural(kc, L: int, plan: Plan, complex_filter: bool = False):
+    """Kernel-order spectrum from the unnormalised natural-order spectrum kc [H, 2L] complex64 of
+    a real filter; with complex_filter, of any filter (the whole spectrum of
+    sffft_spectrum_from_natural_complex, for complex_conv)."""
     import torch
 
     assert kc.is_cuda and kc.dtype == torch.complex64 and kc.shape[1] == 2 * L
     kc = kc.contiguous()
     kf = torch.empty_like(kc)
-    _check(lib().sffft_spectrum_from_natural(_ptr(kc), kc.shape[0], L, ctypes.byref(plan), _ptr(kf), _stream()),
-           "sffft_spectrum_from_natural")
+    fn = lib().sffft_spectrum_from_natural_complex if complex_filter else lib().sffft_spectrum_from_natural
+    _check(fn(_ptr(kc), kc.shape[0], L, ctypes.byref(plan), _ptr(kf), _stream()), "sffft_spectrum_from_natural")
     return kf
 
 
@@ -305,6 +321,7 @@ def conv(u, kf, plan: Plan, out=None, work=None):
     assert u.is_cuda and u.dim() == 3
     u = u.contiguous()
     B, H, L = u.shape
+    _check_spectrum(kf, u, H, 2 * L)
     y = torch.empty_like(u) if out is None else out
     if plan.mode == 2:
         return conv_long(u, kf, plan, y, work)
@@ -324,6 +341,7 @@ def conv_long(u, kf, plan: Plan, out=None, work=None):
 
     u = u.contiguous()
     B, H, L = u.shape
+    _check_spectrum(kf, u, H, 2 * L)
     y = torch.empty_like(u) if out is None else out
     nbytes = work_bytes(B, H, L, plan)
     if work is None:
@@ -366,6 +384,7 @@ def complex_conv(x, kf, plan: Plan):
     import torch
 
     Bc, H, L = x.shape
+    _check_spectrum(kf, x, H, 2 * L)
     u = torch.stack([x.real, x.imag], 1).reshape(2 * Bc, H, L).contiguous()
     if plan.mode == 2:
         y = conv_long(u, kf, plan)

@@ -340,17 +340,18 @@ __global__ void spectrum_permute_kernel(const float2* __restrict__ src, float2* 
 // float4; float4 (k0*PITCH + (kt*2 + q)*4 + g) holds k1 = 16kt + 4g + 2q and +1, i.e.
 // K[k0 + r0*k1]. Column r0/2 holds conj(K[r0/2 + r0*(r1 - 1 - k1)]) at k1; the last float4
 // of each column is zero padding. src as in spectrum_permute_kernel, for the H channels
-// from channel h0 on; channels are consecutive in kf (C = 2*(r0/2 + 1)*PITCH complex
-// values each).
+// from channel h0 on. Each channel keeps its own row of the [H][N] complex64 buffer: its
+// C = 2*(r0/2 + 1)*PITCH values first, zeros after them, so a row of kf is a channel for
+// every plan (slices and concatenations of spectra along the channels stay valid).
 __global__ void spectrum_half_kernel(const float2* __restrict__ src, float2* __restrict__ kf, int H, int h0, int r0,
                                      int r1, float scale, float iscale) {
   const int pitch = 8 * (r1 / 16) + 1, C = 2 * (r0 / 2 + 1) * pitch, N = r0 * r1;
   const size_t gid = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (gid >= (size_t)H * C) return;
-  float2* out = kf + (size_t)h0 * C + gid;
-  const int h = (int)(gid / C), i = (int)(gid % C);
+  if (gid >= (size_t)H * N) return;
+  float2* out = kf + (size_t)h0 * N + gid;
+  const int h = (int)(gid / N), i = (int)(gid % N);
   const int f = i >> 1, e = i & 1, k0 = f / pitch, rem = f % pitch;
-  if (rem == pitch - 1) {
+  if (i >= C || rem == pitch - 1) {
     *out = make_float2(0.f, 0.f);
     return;
   }
@@ -361,13 +362,6 @@ __global__ void spectrum_half_kernel(const float2* __restrict__ src, float2* __r
   const int sidx = k0 + r0 * kk1;
   const float2 v = src[(size_t)h * N + sidx];
   *out = make_float2(v.x * scale, (mid ? -v.y : v.y) * iscale);
-}
-
-// Zeroes n complex values (the part of a spectrum buffer a Hermitian half leaves unused,
-// so the whole buffer is a function of the filter); a kernel, so it can be captured.
-__global__ void zero_fill_kernel(float2* __restrict__ p, size_t n) {
-  const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i < n) p[i] = make_float2(0.f, 0.f);
 }
 
 // Filter rows kr[h][0..klen) (+ i ki[h][..] for a complex filter, ki may be null) as complex
@@ -398,6 +392,28 @@ float last_stage_scale(const sffft_plan* p) {
 }
 
 bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+// Test probe of the in-register twiddles of the workgroup kernel (fftconv.hpp): query q =
+// (e0, step, f0, fstep) gives the four values twiddle4e<N>(e0, step, sc) and `rows` row
+// steps, each the complex product with twiddle4e<N>(f0, fstep, 1) (the row recurrence of the
+// kernel's phase-2 loop), stored as out[q][row][v] complex64, row = 0..rows.
+template <int N>
+__global__ void twiddle_probe_kernel(const int4* __restrict__ qs, float2* __restrict__ out, int nq, int rows,
+                                     float sc) {
+  const int q = blockIdx.x * blockDim.x + threadIdx.x;
+  if (q >= nq) return;
+  const int4 a = qs[q];
+  float wr[4], wi[4], fr[4], fi[4];
+  twiddle4e<N>(a.x, a.y, sc, wr, wi);
+  twiddle4e<N>(a.z, a.w, 1.f, fr, fi);
+  float2* o = out + (size_t)q * (rows + 1) * 4;
+  for (int r = 0;; r++) {
+#pragma unroll
+    for (int v = 0; v < 4; v++) o[r * 4 + v] = make_float2(wr[v], wi[v]);
+    if (r == rows) break;
+    cmul4(wr, wi, fr, fi);
+  }
+}
 
 // Body-less kernel: launched with a plan's grid, block and LDS size it measures the
 // dispatch cost of that launch shape (workgroup dispatch, LDS allocation, wave
@@ -488,40 +504,30 @@ int long_plans_for(int L, const LongEntry** out, int cap) {
 // Launches the gather of a natural-order spectrum src of the H channels from channel h0 on
 // into the kernel order of the plan: the Hermitian half for wave plans (mode 1) unless
 // `whole` (complex filters), else the whole spectrum; with conj, of the conjugate spectrum.
-// kf is the spectrum of all Htot channels; the gather of the last channels also zeroes what
-// a Hermitian half leaves unused.
+// Channel h is row h of kf ([H][N] complex64) in every case.
 int permute_launch(const float2* src, float2* kf, int H, const sffft_plan* plan, int whole, int conj, hipStream_t s,
-                   int h0 = 0, int Htot = -1) {
+                   int h0 = 0) {
   const float sc = last_stage_scale(plan), isc = conj ? -sc : sc;
-  if (Htot < 0) Htot = H;
-  const size_t N = (size_t)plan->r0 * plan->r1 * plan->r2;
-  if (plan->mode == 1 && !whole) {
-    const size_t C = (size_t)2 * (plan->r0 / 2 + 1) * (8 * (plan->r1 / 16) + 1), total = (size_t)H * C;
+  const size_t N = (size_t)plan->r0 * plan->r1 * plan->r2, total = (size_t)H * N;
+  if (plan->mode == 1 && !whole)
     hipLaunchKernelGGL(spectrum_half_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, src, kf, H, h0,
                        plan->r0, plan->r1, sc, isc);
-    if (h0 + H == Htot) {
-      const size_t tail = (size_t)Htot * (N - C);
-      hipLaunchKernelGGL(zero_fill_kernel, dim3((unsigned)((tail + 255) / 256)), dim3(256), 0, s,
-                         kf + (size_t)Htot * C, tail);
-    }
-  } else {
-    const size_t total = (size_t)H * N;
+  else
     hipLaunchKernelGGL(spectrum_permute_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, src,
                        kf + (size_t)h0 * N, H, plan->r0, plan->r1, plan->r2, plan->mode, sc, isc);
-  }
   return hip_status(hipGetLastError(), "spectrum permute launch");
 }
 
-// Spectrum of the H filter rows from channel h0 on (all Htot of them when Htot < 0): kr, plus
+// Spectrum of the H filter rows from channel h0 on: kr, plus
 // i ki for a complex filter (ki non-null, whole spectrum); with conj, its conjugate (the
 // spectrum the correlations of the backward passes run on). The padded rows are transformed
 // in place in `work` (H * N complex64; fp64 stages, complex64 between them), then gathered
 // into kernel order. Up to 16384 points the transform is one pass through LDS and needs no
 // workspace. Longer rows take the staged transform, whose workspace is this call's own rows
-// of kf: the gather overwrites them afterwards, and the results of earlier calls (channels
-// before h0, at most h0 * N values even as Hermitian halves) lie before them.
+// of kf: the gather overwrites them afterwards, and the results of earlier calls (the rows
+// of the channels before h0) lie before them.
 int spectrum_impl(const float* kr, const float* ki, int H, int L, int klen, const sffft_plan* plan, void* kf,
-                  void* work, void* stream, int whole = 0, int conj = 0, int h0 = 0, int Htot = -1) {
+                  void* work, void* stream, int whole = 0, int conj = 0, int h0 = 0) {
   if (!kr || !kf || !work || H < 1 || kf == work) return SFFFT_EINVAL;
   const int rc = check_shape(L, plan);
   if (rc) return rc;
@@ -536,7 +542,7 @@ int spectrum_impl(const float* kr, const float* ki, int H, int L, int klen, cons
   const xf::Seqs q{H, 1, 0, N, 1, 0};
   float2* scratch = N <= xf::ONEPASS_MAX_N ? nullptr : static_cast<float2*>(kf) + (size_t)h0 * N;
   if ((st = hip_status(xf::run(w, w, scratch, q, N, 0, 1.f, s), "spectrum transform launch"))) return st;
-  return permute_launch(w, static_cast<float2*>(kf), H, plan, whole, conj, s, h0, Htot);
+  return permute_launch(w, static_cast<float2*>(kf), H, plan, whole, conj, s, h0);
 }
 }  // namespace
 }  // namespace sffft
@@ -638,7 +644,7 @@ int sffft_spectrum_noalloc(const float* k, int H, int L, const sffft_plan* plan,
   if ((rc = scratch_for_device(&work))) return rc;
   const int chunk = (int)std::min<size_t>((size_t)H, SFFFT_SCRATCH_BYTES / per);
   for (int h0 = 0; h0 < H; h0 += chunk)
-    if ((rc = spectrum_impl(k, nullptr, std::min(chunk, H - h0), L, L, plan, kf, work, stream, 0, 0, h0, H)))
+    if ((rc = spectrum_impl(k, nullptr, std::min(chunk, H - h0), L, L, plan, kf, work, stream, 0, 0, h0)))
       return rc;
   return SFFFT_OK;
 }
@@ -673,6 +679,15 @@ int sffft_spectrum_from_natural(const void* kc, int H, int L, const sffft_plan* 
   const int rc = check_shape(L, plan);
   if (rc) return rc;
   return permute_launch(static_cast<const float2*>(kc), static_cast<float2*>(kf), H, plan, 0, 0,
+                        (hipStream_t)stream);
+}
+
+int sffft_spectrum_from_natural_complex(const void* kc, int H, int L, const sffft_plan* plan, void* kf,
+                                        void* stream) {
+  if (!kc || !kf || H < 1 || kc == kf || !plan || plan->seqs != 2) return SFFFT_EINVAL;
+  const int rc = check_shape(L, plan);
+  if (rc) return rc;
+  return permute_launch(static_cast<const float2*>(kc), static_cast<float2*>(kf), H, plan, 1, 0,
                         (hipStream_t)stream);
 }
 
@@ -742,10 +757,12 @@ bool span_overlap(const void* a, size_t na, const void* b, size_t nb) {
 }
 bool aligned8(const void* p) { return ((uintptr_t)p & 7u) == 0; }
 
-// Validated 1-D transform layout; *extent: extent of x / X in complex elements. The layout
-// must be one-to-one (no two (sequence, element) pairs at one address): each sequence
-// whole before the next (dist >= N * stride), or the sequences interleaved within one
-// element step (stride >= batch * dist), as the columns of a row-major matrix are.
+// Validated 1-D transform layout; *extent: extent of x / X in complex elements. Two layout
+// families are supported, both one-to-one (no two (sequence, element) pairs at one
+// address): each sequence whole before the next (dist >= N * stride), or the sequences
+// interleaved within one element step (stride >= batch * dist), as the columns of a
+// row-major matrix are. Other layouts are rejected, also the non-overlapping ones between
+// the two families (batch 3, N 4, stride 2, dist 5 is one).
 int fft_layout(int batch, int N, long long stride, long long dist, xf::Seqs* q, long long* extent) {
   xf::Radices d;
   if (batch < 1 || !xf::split(N, &d) || (long long)batch * N > xf::MAX_ELEMS) return SFFFT_EINVAL;
@@ -858,6 +875,36 @@ int sffft_dft_table(void* out, size_t out_len) {
   const int rc = device_table(&table);
   if (rc) return rc;
   return hip_status(hipMemcpy(out, table, bytes, hipMemcpyDeviceToHost), "hipMemcpy");
+}
+
+int sffft_twiddle_probe(int N, const void* queries, int nq, int rows, float sc, void* out, void* stream) {
+  if (!queries || !out || nq < 1 || rows < 0 || rows > 64) return SFFFT_EINVAL;
+  const dim3 grid((unsigned)((nq + 63) / 64)), block(64);
+  const int4* q = static_cast<const int4*>(queries);
+  float2* o = static_cast<float2*>(out);
+  hipStream_t s = (hipStream_t)stream;
+  switch (N) {
+    case 256: hipLaunchKernelGGL(twiddle_probe_kernel<256>, grid, block, 0, s, q, o, nq, rows, sc); break;
+    case 512: hipLaunchKernelGGL(twiddle_probe_kernel<512>, grid, block, 0, s, q, o, nq, rows, sc); break;
+    case 1024: hipLaunchKernelGGL(twiddle_probe_kernel<1024>, grid, block, 0, s, q, o, nq, rows, sc); break;
+    case 2048: hipLaunchKernelGGL(twiddle_probe_kernel<2048>, grid, block, 0, s, q, o, nq, rows, sc); break;
+    case 4096: hipLaunchKernelGGL(twiddle_probe_kernel<4096>, grid, block, 0, s, q, o, nq, rows, sc); break;
+    case 8192: hipLaunchKernelGGL(twiddle_probe_kernel<8192>, grid, block, 0, s, q, o, nq, rows, sc); break;
+    case 16384: hipLaunchKernelGGL(twiddle_probe_kernel<16384>, grid, block, 0, s, q, o, nq, rows, sc); break;
+    case 32768: hipLaunchKernelGGL(twiddle_probe_kernel<32768>, grid, block, 0, s, q, o, nq, rows, sc); break;
+    default: return SFFFT_EINVAL;
+  }
+  return hip_status(hipGetLastError(), "twiddle probe launch");
+}
+
+int sffft_twiddle_table(int r0, int r1, int split, void* out, size_t out_len) {
+  if (!valid_radix(r0) || !valid_radix(r1) || (split != 0 && split != 1) || !out) return SFFFT_EINVAL;
+  const size_t bytes = (size_t)r0 * r1 * 16;  // two tables of N complex fp32
+  if (out_len < bytes) return SFFFT_EINVAL;
+  const void* tw = nullptr;
+  const int rc = device_twiddles(r0, r1, split != 0, &tw);
+  if (rc) return rc;
+  return hip_status(hipMemcpy(out, tw, bytes, hipMemcpyDeviceToHost), "hipMemcpy");
 }
 
 int sffft_select_candidate(const sffft_candidate* c, int n, double max_error, const char* io) {

@@ -1070,7 +1070,8 @@ __global__ void __launch_bounds__(64 * NW, WPE)
   if constexpr (P::S == 2) {
     KData2<P, NW> kd;
     k_prefetch_s2<P, NW>(K, kd, lane, wave);
-    phase1<P, NW, NSEQ, TIO, CACHED, false>(ad, fr, re, im, ftab, acc16, lane, wave);
+    phase1<P, NW, NSEQ, TIO, CACHED, sizeof(TIO) == 4 && (SFFFT_FP32_SPLITS & 8)>(ad, fr, re, im, ftab, acc16, lane,
+                                                                                   wave);
     __syncthreads();
     phase2_s2<P, NW, CACHED, sizeof(TIO) == 4>(re, im, kd, ftab, acc16, lane, wave);
   } else {

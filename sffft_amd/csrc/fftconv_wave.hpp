@@ -304,9 +304,12 @@ __device__ __forceinline__ float io_to_f32_lds(const float* p) { return *p; }
 __device__ __forceinline__ float io_to_f32_lds(const uint16_t* p) { return __uint_as_float((uint32_t)*p << 16); }
 
 // Phase-1 A operands a[mt][ks] (slots 0..3 row a, 4..7 row b; n0 = 16ks + 4g + j,
-// m = 16mt + r) from the pair's chunks, through the wave's scratch S.
-template <class P, class TIO>
-__device__ __forceinline__ void pair_operands(const PairLoads<P, TIO>& d, TIO* S, h8 (*a)[P::KS1], int lane) {
+// m = 16mt + r) from the pair's chunks, through the wave's scratch S. With SPLIT each
+// fp32 sample x enters as fp16(x) in a and its remainder fp16(x - fp16(x)) in alo, so
+// that phase 1 sees x to about 22 bits instead of 11.
+template <class P, class TIO, bool SPLIT>
+__device__ __forceinline__ void pair_operands(const PairLoads<P, TIO>& d, TIO* S, h8 (*a)[P::KS1],
+                                              h8 (*alo)[P::KS1], int lane) {
   typedef PairLoads<P, TIO> D;
   constexpr int R0 = P::R0, M = P::M, PITCH = scratch_pitch<P, TIO>();
   constexpr int ROWS = R0 / 2 < 16 ? R0 / 2 : 16;  // non-zero rows per K step
@@ -336,7 +339,9 @@ __device__ __forceinline__ void pair_operands(const PairLoads<P, TIO>& d, TIO* S
         for (int j = 0; j < 4; j++) {
           const bool live = 4 * g + j < ROWS;
           const float v = live ? io_to_f32_lds(S + (4 * g + j) * PITCH + 16 * mt + r) : 0.f;
-          a[mt][ks][4 * sq + j] = (_Float16)v;
+          const _Float16 hi = (_Float16)v;
+          a[mt][ks][4 * sq + j] = hi;
+          if constexpr (SPLIT) alo[mt][ks][4 * sq + j] = (_Float16)(v - (float)hi);
         }
       wave_lds_fence();
     }
@@ -374,8 +379,9 @@ __device__ __forceinline__ void store_rows(TIO* S, const f4 (&z)[P::MT], TIO* __
 }
 
 // Every stage of one pair, from its loaded operands to the stored outputs; SP is the
-// channel's spectrum in LDS.
-template <class P, class TIO, bool ACC16, bool HOLD_F1, bool K1, bool HERM>
+// channel's spectrum in LDS. SPLIT: fp32 input as value plus remainder (pair_operands),
+// two MFMAs per phase-1 product into the same accumulator.
+template <class P, class TIO, bool ACC16, bool HOLD_F1, bool K1, bool HERM, bool SPLIT>
 __device__ __forceinline__ void process_pair(const PairLoads<P, TIO>& d, TIO* S, const float4* SP,
                                              TIO* __restrict__ ya, TIO* __restrict__ yb, const h8* F0,
                                              const h8* F1, const float4* TW1, const float4* TW2, int lane) {
@@ -390,8 +396,8 @@ __device__ __forceinline__ void process_pair(const PairLoads<P, TIO>& d, TIO* S,
   };
 
   // ---- phase 1: DFT over n0 (first R0/2 rows only), twiddle, -> B2[m tile][k0 strip]
-  h8 a[MT][KS1];
-  pair_operands<P, TIO>(d, S, a, lane);
+  h8 a[MT][KS1], alo[SPLIT ? MT : 1][KS1];
+  pair_operands<P, TIO, SPLIT>(d, S, a, alo, lane);
   h8 b2[MT][ST];
 #pragma unroll
   for (int nt = 0; nt < ST; nt++) {
@@ -409,6 +415,10 @@ __device__ __forceinline__ void process_pair(const PairLoads<P, TIO>& d, TIO* S,
       for (int ks = 0; ks < KS1; ks++) {
         dr = mfma(a[mt][ks], f0[ks], dr);
         di = mfma(a[mt][ks], f1[ks], di);
+        if constexpr (SPLIT) {
+          dr = mfma(alo[mt][ks], f0[ks], dr);
+          di = mfma(alo[mt][ks], f1[ks], di);
+        }
       }
       dr = acc_round<ACC16>(dr);
       di = acc_round<ACC16>(di);
@@ -520,8 +530,9 @@ __device__ __forceinline__ void process_pair(const PairLoads<P, TIO>& d, TIO* S,
 // and (2bp+1, h), h = w*CH + c. Wave v takes pairs v, v + NW, ... The DFT and
 // twiddle tables and the CH channel spectra are copied into LDS once, so the
 // B/2 wavefronts of a channel read its spectrum from LDS rather than each from L2.
-// HERM: kf holds Hermitian half spectra (real filters, hs_index, HSP_F4 float4 per
-// channel); otherwise whole spectra (complex filters, sp_index, SP_F4 per channel).
+// HERM: kf holds Hermitian half spectra (real filters, hs_index, HSP_F4 float4 at the
+// start of each channel's row); otherwise whole spectra (complex filters, sp_index, SP_F4
+// per channel). The rows of kf are SP_F4 float4 (2L complex64) apart in both cases.
 template <class P, int NW, int CH, class TIO, bool CACHED, bool ACC16, bool HERM>
 __global__ void __launch_bounds__(64 * NW)
     fftconv_wave_kernel(const TIO* __restrict__ u, const float4* __restrict__ kf, TIO* __restrict__ y, int B,
@@ -559,18 +570,22 @@ __global__ void __launch_bounds__(64 * NW)
     if constexpr (P::R1 != P::R0)
       dma_to_lds<F1_H8, NW>(reinterpret_cast<float4*>(F1), [&](int k) { return tab(P::R1, k); }, lane, wave);
   }
+  // channel h's spectrum (SPC_F4 float4) starts row h of the caller's [H][2L] complex64
+  // buffer, whose rows are SP_F4 float4 apart
   if constexpr (SP_LDS) {
-    // channel c of this workgroup is in slot c (the channels' spectra are consecutive in
-    // global memory); what the copy's whole runs add past the last channel repeats the
-    // last float4 of the last channel (in bounds, never read)
-    const float4* src = kf + (size_t)h0 * SPC_F4;
+    // channel c of this workgroup goes to LDS slot c, the slots consecutive; what the
+    // copy's whole runs add past the last channel repeats the last float4 of the last
+    // channel (in bounds, never read)
     const int last = nch * SPC_F4 - 1;
-    dma_to_lds<SPL_F4, NW>(SPL, [&](int k) { return src + (k < last ? k : last); }, lane, wave);
+    dma_to_lds<SPL_F4, NW>(SPL, [&](int k) {
+      const int kk = k < last ? k : last, c = kk / SPC_F4;
+      return kf + (size_t)(h0 + c) * P::SP_F4 + (kk - c * SPC_F4);
+    }, lane, wave);
   }
   // spectrum of channel slot c: in LDS, or the channel's row in global memory
   auto spec = [&](int c) -> const float4* {
     if constexpr (SP_LDS) return SPL + c * SPC_F4;
-    else return kf + (size_t)(h0 + c) * SPC_F4;
+    else return kf + (size_t)(h0 + c) * P::SP_F4;
   };
   if constexpr (!CACHED) {
     compute_dft<R0, 64 * NW, K1>(F0, tid);
@@ -614,10 +629,16 @@ __global__ void __launch_bounds__(64 * NW)
   // radix-R1 axis: 32 VGPRs, within the budget of three wavefronts per SIMD (64x32 with
   // 12 wavefronts: 150 VGPRs; measured 1-2% faster with bf16 I/O, equal with fp32)
   constexpr bool HOLD = P::MT <= 2;
+  // fp32 input split into value and remainder where the launch is bound by its dispatch
+  // floor and HBM, not by the SIMDs (L <= 512): removes the input's fp16 rounding, one of
+  // the four roundings of a two-stage plan, for twice the phase-1 MFMAs (a quarter of
+  // the pair's). bf16 samples are exact in fp16; the fp16-accumulation mode keeps the
+  // one rounding.
+  constexpr bool SPLIT = sizeof(TIO) == 4 && !ACC16 && P::L <= 512;
   if (wave < npairs) {
     const int c = wave / BP, bp = wave - c * BP;
     const size_t ra = ((size_t)(2 * bp) * H + h0 + c) * P::L, rb = ra + (size_t)H * P::L;
-    process_pair<P, TIO, ACC16, HOLD, K1, HERM>(cur, S, spec(c), y + ra, y + rb, F0, F1, TW1, TW2, lane);
+    process_pair<P, TIO, ACC16, HOLD, K1, HERM, SPLIT>(cur, S, spec(c), y + ra, y + rb, F0, F1, TW1, TW2, lane);
   }
   for (int p = wave + NW; p < npairs; p += NW) {
     // compiler-only barrier: keeps the table reads inside the loop (hoisting them
@@ -631,7 +652,7 @@ __global__ void __launch_bounds__(64 * NW)
     const int c = p / BP, bp = p - c * BP;
     const size_t ra = ((size_t)(2 * bp) * H + h0 + c) * P::L, rb = ra + (size_t)H * P::L;
     issue_pair_loads<P, TIO>(u + ra, u + rb, cur, ln);
-    process_pair<P, TIO, ACC16, HOLD, K1, HERM>(cur, S, spec(c), y + ra, y + rb, F0, F1, TW1, TW2, ln);
+    process_pair<P, TIO, ACC16, HOLD, K1, HERM, SPLIT>(cur, S, spec(c), y + ra, y + rb, F0, F1, TW1, TW2, ln);
   }
 }
 

@@ -75,6 +75,10 @@ at::Tensor conv_gpu(const at::Tensor& u_in, const at::Tensor& kf, c10::IntArrayR
   const at::Tensor u = u_in.contiguous();
   const int64_t B = u.size(0), H = u.size(1), L = u.size(2);
   TORCH_CHECK(B <= INT32_MAX && H <= INT32_MAX && L <= INT32_MAX, "sffft::conv: shape too large");
+  // the kernels read H rows of 2L values from the start of kf (row h is channel h's
+  // spectrum): a spectrum of fewer channels or of another length would be read past its end
+  TORCH_CHECK(kf.dim() == 2 && kf.size(0) == H && kf.size(1) == 2 * L, "sffft::conv: kf must be [H, 2L] = [", H,
+              ", ", 2 * L, "] for u of shape ", u.sizes(), ", got ", kf.sizes());
   const sffft_plan p = to_plan(plan_fields);
   at::Tensor y = at::empty_like(u);
   const bool bf16 = u.scalar_type() == at::kBFloat16;

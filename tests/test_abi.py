@@ -76,6 +76,13 @@ def test_conv_argument_errors_need_no_gpu():
                               null) == sf.SFFFT_EINVAL  # misaligned rows
     assert lib.sffft_conv_bf16(good, good, good, 0, 768, 1024, ctypes.byref(p), null) == sf.SFFFT_EINVAL
     assert lib.sffft_spectrum(good, 768, 1024, ctypes.byref(p), good, good, null) == sf.SFFFT_EINVAL  # kf == work
+    # the whole-spectrum gather serves pair plans only, and kc and kf must differ
+    f = lib.sffft_spectrum_from_natural_complex
+    assert f(good, 768, 1024, ctypes.byref(sf.make_plan("64x32", 4, seqs=1)), ctypes.c_void_p(1 << 30),
+             null) == sf.SFFFT_EINVAL
+    assert f(good, 768, 1024, ctypes.byref(p), good, null) == sf.SFFFT_EINVAL
+    assert f(null, 768, 1024, ctypes.byref(p), good, null) == sf.SFFFT_EINVAL
+    assert f(good, 768, 1000, ctypes.byref(p), ctypes.c_void_p(1 << 30), null) == sf.SFFFT_EINVAL
     assert sf.lib().sffft_spectrum_bytes(768, 1024) == 768 * 2048 * 8
     # the dispatch floor checks its shape like conv, before any HIP call
     assert lib.sffft_dispatch_floor(0, 768, 1024, ctypes.byref(p), null) == sf.SFFFT_EINVAL

@@ -105,8 +105,11 @@ def test_spectrum_from_natural_is_the_digit_permutation(dev, L, plan):
     sc = last_stage_scale(plan)
     freq = np.array([o[0] for o in order])
     conj = np.array([o[1] for o in order])
+    assert kf.shape == (H, N), "one row per channel"
     for ch in range(H):
-        got = kf.reshape(-1)[ch * n:(ch + 1) * n]
+        got = kf[ch, :n]
+        # a Hermitian half leaves the rest of its channel's row zero
+        assert np.all(kf[ch, n:] == 0), (L, plan)
         pad = freq < 0
         assert np.all(got[pad] == 0), "padding slots are zero"
         fr = freq[~pad]
@@ -130,7 +133,7 @@ def test_half_spectrum_matches_whole_spectrum(dev, L):
     H = 5
     k = torch.from_numpy(np.random.default_rng(L).standard_normal((H, L)).astype(np.float32)).to(dev)
     for plan in [p for p in sf.plans(L) if p.mode == 1]:
-        half = sf.spectrum(k, L, plan).cpu().numpy().reshape(-1)
+        half = sf.spectrum(k, L, plan).cpu().numpy()
         whole = sf.spectrum_complex(torch.complex(k, torch.zeros_like(k)), L, plan).cpu().numpy()
         order = kernel_order(plan)
         n = len(order)
@@ -145,7 +148,8 @@ def test_half_spectrum_matches_whole_spectrum(dev, L):
             k1 = 16 * (tile % MT) + 4 * g + 2 * q + e
             pos[k0 + plan.r0 * k1] = idx
         for ch in range(H):
-            got = half[ch * n:(ch + 1) * n]
+            got = half[ch, :n]
+            assert np.all(half[ch, n:] == 0)
             for i, (fr, cj) in enumerate(order):
                 if fr < 0:
                     continue

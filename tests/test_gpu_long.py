@@ -181,12 +181,23 @@ def test_circular_conv_matches_oracle(dev, N, spec):
     assert oracle.rel_l2(y[..., :L], ref_causal) <= 5e-4
 
 
-@pytest.mark.parametrize("L,plan_of", [(1024, lambda L: sf.default_plan(L)), (4096, lambda L: sf.default_plan(L)),
-                                        (32768, lambda L: sf.default_plan(L))],
-                         ids=["L1024-wave", "L4096-workgroup", "L32768-multipass"])
+@pytest.mark.parametrize("L,plan_of", [
+    (128, lambda L: sf.default_plan(L)),
+    (256, lambda L: sf.make_plan("16x32", 12, seqs=2, mode=1, channels=3)),
+    (512, lambda L: sf.make_plan("64x16", 12, seqs=2, mode=1, channels=3)),
+    (1024, lambda L: sf.default_plan(L)),
+    (2048, lambda L: sf.default_plan(L)),
+    (4096, lambda L: sf.default_plan(L)),
+    (32768, lambda L: sf.default_plan(L))],
+    ids=["L128-wave16x16", "L256-wave16x32", "L512-wave64x16", "L1024-wave", "L2048-wave64x64-spectraL2",
+         "L4096-workgroup", "L32768-multipass"])
 def test_complex_input_conv(dev, L, plan_of):
     """Complex causal convolution (sffft_spectrum_complex + a pair plan): complex u and complex
-    k, every output against numpy's fp64 complex convolution."""
+    k, every output against numpy's fp64 complex convolution. The wave plans run their
+    whole-spectrum instantiation: R0 = 16 (one strip split at lane 8 in the Hermitian form),
+    R1 = 32 with R0 = 16, 64x16, and 64x64 (whole spectra read through L2, first-kind
+    fragments only). The same spectrum gathered from torch's natural-order spectrum
+    (sffft_spectrum_from_natural_complex) agrees with it to fp32 rounding."""
     import torch
 
     plan = plan_of(L)
@@ -195,7 +206,13 @@ def test_complex_input_conv(dev, L, plan_of):
     x = (rng.standard_normal((Bc, H, L)) + 1j * rng.standard_normal((Bc, H, L))).astype(np.complex64)
     env = np.exp(-np.arange(L) / (L / 8)) / np.sqrt(L)
     k = ((rng.standard_normal((H, L)) + 1j * rng.standard_normal((H, L))) * env).astype(np.complex64)
-    kf = sf.spectrum_complex(torch.from_numpy(k).to(dev), L, plan)
+    kd = torch.from_numpy(k).to(dev)
+    kf = sf.spectrum_complex(kd, L, plan)
+    if L <= 16384:
+        kc = torch.fft.fft(torch.cat([kd, torch.zeros_like(kd)], 1), dim=1)  # zero-padded to 2L
+        kf_nat = sf.spectrum_from_natural(kc, L, plan, complex_filter=True)
+        # the spectrum's own transform and rocFFT's differ in their last bits: compare as values
+        assert torch.allclose(torch.view_as_real(kf_nat), torch.view_as_real(kf), rtol=1e-5, atol=1e-6)
     y = sf.complex_conv(torch.from_numpy(x).to(dev), kf, plan).cpu().numpy().astype(np.complex128)
     x64, k64 = x.astype(np.complex128), k.astype(np.complex128)
     if L <= 4096:

@@ -8,9 +8,10 @@ driver (`sffft`, the reference's CLI) on the reference's own input generator
   plan is a statistical quantity of the schedule, so a one-sequence plan must land within
   25% of the published value. A plan that packs two sequences into one transform carries
   about 1.2x the one-sequence noise (the imaginary half of each transform holds the second
-  sequence), and the three-stage plans feed the fp32 input as an fp16 value plus its
-  remainder (lower error); both are held to [0.75, 1.5] of the published value. bf16 I/O
-  errors are dominated by the I/O rounding and must land within 25% in every case.
+  sequence); the three-stage plans and the wave plans up to L = 512 feed the fp32 input as
+  an fp16 value plus its remainder, which removes one of their fp16 roundings. Every plan
+  is held to [0.75, 1.25] of the published value. bf16 I/O errors are dominated by the I/O
+  rounding and must land within 25% in every case.
 - the speed target of the fused kernel: the selected fused candidate at least 4x faster than
   the rocFFT pad/R2C/multiply/C2R/slice pipeline at every L of the reference's sweep
   (src/sffft.cu:372-381,506-513), for fp32 and bf16 I/O.
@@ -75,16 +76,10 @@ def test_per_plan_errors_match_the_published_values(dev):
         pub = PUBLISHED.get((L, plan))
         if pub is None:
             continue
-        seqs = int([f for f in cfg.split("/") if f.startswith("seq")][0][3:])
-        if r[2] == "fused_fp32io":
-            ratio = err / pub[0]
-            lo, hi = (0.75, 1.25) if seqs == 1 else (0.75, 1.5)
-        else:
-            ratio = err / pub[1]
-            lo, hi = 0.75, 1.25
-        print(f"L={L} {r[2]} {cfg}: {err:.3e} / published {pub[0] if r[2] == 'fused_fp32io' else pub[1]:.3e} "
-              f"= {ratio:.3f}", flush=True)
-        assert lo <= ratio <= hi, (L, r[2], cfg, err, pub)
+        published = pub[0] if r[2] == "fused_fp32io" else pub[1]
+        ratio = err / published
+        print(f"L={L} {r[2]} {cfg}: {err:.3e} / published {published:.3e} = {ratio:.3f}", flush=True)
+        assert 0.75 <= ratio <= 1.25, (L, r[2], cfg, err, pub)
         checked += 1
     assert checked >= 2 * len(PUBLISHED) - 8, checked  # nearly every published plan is compiled here
 

@@ -76,6 +76,34 @@ def test_one_pass_matches_staged_path_bitwise(batch, N):
         assert np.array_equal(a.view(np.uint32), b.view(np.uint32)), (N, inverse)
 
 
+@pytest.mark.parametrize("batch,N,stride,dist", [(3, 128, 2, 256), (3, 128, 3, 1), (2, 4096, 3, 12288),
+                                                  (4, 256, 4, 1)])
+def test_fft_layout_family_edges(batch, N, stride, dist):
+    """The edges of the two layout families sffft_fft_c2c takes: whole sequences exactly
+    N * stride apart, and sequences interleaved exactly batch * dist per element step. Gaps
+    in the layout stay untouched."""
+    import ctypes
+
+    print(f"fft layout batch={batch} N={N} stride={stride} dist={dist}", flush=True)
+    extent = (batch - 1) * dist + (N - 1) * stride + 1
+    rng = np.random.default_rng(N + stride)
+    buf = crandn(rng, extent)
+    idx = np.array([[b * dist + n * stride for n in range(N)] for b in range(batch)])
+    x = torch.from_numpy(buf).to(DEV)
+    X = torch.full_like(x, complex(7.0, -3.0))
+    work = torch.empty(max(sf.lib().sffft_fft_work_bytes(batch, N), 16), dtype=torch.uint8, device=DEV)
+    rc = sf.lib().sffft_fft_c2c(ctypes.c_void_p(x.data_ptr()), ctypes.c_void_p(X.data_ptr()),
+                                ctypes.c_void_p(work.data_ptr()), work.numel(), batch, N, stride, dist, 0, 1.0,
+                                ctypes.c_void_p(0))
+    assert rc == sf.SFFFT_OK, sf.strerror(rc)
+    out = X.cpu().numpy()
+    ref = np.fft.fft(buf[idx].astype(np.complex128), axis=1)
+    assert rel(out[idx], ref) <= 1e-6
+    untouched = np.ones(extent, bool)
+    untouched[idx.reshape(-1)] = False
+    assert np.all(out[untouched] == np.complex64(complex(7.0, -3.0)))
+
+
 @pytest.mark.parametrize("L", [128, 1024, 8192, 16384, 32768])
 def test_spectrum_matches_fp64_dft(L):
     """sffft_spectrum against the same kernel-order gather (sffft_spectrum_from_natural)

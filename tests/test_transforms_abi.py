@@ -53,3 +53,30 @@ def test_argument_errors_need_no_gpu():
     assert c(x, X, ctypes.c_void_p((1 << 40) + (1 << 36)), w, need - 8, 2, 3, 64, 128, null) == E  # too small
     assert c(x, X, ctypes.c_void_p((1 << 40) + 64), w, need, 2, 3, 64, 128, null) == E           # y overlaps u
     assert c(x, X, ctypes.c_void_p((1 << 40) + (1 << 36)), w, need, 2, 3, 64, 96, null) == E     # N1 invalid
+
+
+def test_layout_families():
+    """sffft_fft_c2c takes two layout families: whole sequences one after another
+    (dist >= N * stride) and sequences interleaved within one element step (stride >=
+    batch * dist). Layouts between them are rejected before any HIP call, including
+    non-overlapping ones."""
+    lib = sf.lib()
+    E = sf.SFFFT_EINVAL
+    null = ctypes.c_void_p(0)
+    x, X, w = (ctypes.c_void_p((1 << 40) + i * (1 << 34)) for i in range(3))
+    f = lib.sffft_fft_c2c
+
+    def disjoint(batch, N, stride, dist):
+        addrs = {b * dist + n * stride for b in range(batch) for n in range(N)}
+        return len(addrs) == batch * N
+
+    # between the families, yet one-to-one: 3 sequences of 4 at stride 2, 5 apart
+    assert disjoint(3, 4, 2, 5)
+    assert f(x, X, w, 1 << 20, 3, 4, 2, 5, 0, 1.0, null) == E
+    # the same with N = 128 (the workspace path): the odd distance interleaves the middle
+    # sequence's elements between the others', and an overlapping one
+    assert disjoint(3, 128, 2, 129)
+    assert f(x, X, w, 1 << 20, 3, 128, 2, 129, 0, 1.0, null) == E
+    assert not disjoint(3, 128, 2, 4)
+    assert f(x, X, w, 1 << 20, 3, 128, 2, 4, 0, 1.0, null) == E
+    # the edges of the two families are accepted: tests/test_gpu_transforms.py runs them
