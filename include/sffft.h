@@ -242,11 +242,13 @@ int sffft_dft_table(void* out, size_t out_len);
  * queries (e0, step, f0, fstep) (device int[4] each): the four values
  * sc * exp(-2 pi i (e0 + step*v) / N), v = 0..3, and `rows` (<= 64) row steps, each the
  * product with exp(-2 pi i (f0 + fstep*v) / N); out is device complex64 [nq][rows+1][4].
- * N a power of two in [256, 32768]. sffft_twiddle_table copies the wave pipeline's fp32
- * twiddle tables of plan r0 x r1 (built in fp64 on the host; layout 1 = split, the wave
- * kernels', 0 = paired, the multi-pass row pass's) to host memory `out`: r0*r1*16 bytes. */
+ * N a power of two in [256, 32768]. sffft_twiddle_table copies the wave pipeline's twiddle
+ * tables of plan r0 x r1 (built in fp64 on the host) to host memory `out`: layout 1 = fp32
+ * split (the wave kernels'), 0 = fp32 paired (64x64 and the multi-pass row pass), r0*r1*16
+ * bytes; 2 = fp16 (the fp16-products wave kernels of bf16 I/O and fp16 accumulation),
+ * r0*r1*8 bytes. */
 int sffft_twiddle_probe(int N, const void* queries, int nq, int rows, float sc, void* out, void* stream);
-int sffft_twiddle_table(int r0, int r1, int split, void* out, size_t out_len);
+int sffft_twiddle_table(int r0, int r1, int layout, void* out, size_t out_len);
 
 /* Host-side selector (src/selection.h:8-29). A candidate is (method, io, config, ms,
  * rel_err); io is "fp32" or "bf16". Returns the index of the fastest candidate whose io

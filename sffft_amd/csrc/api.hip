@@ -235,6 +235,26 @@ void build_twiddles(int r0, int r1, bool split, std::vector<float>& t) {
         }
 }
 
+// Layout 2 (the fp16-products kernels): the same values rounded to fp16, one 16-byte entry
+// per (tile, lane) at h8 index tile * 64 + lane, [wr0 wr1 wr2 wr3 | wi0 wi1 wi2 wi3]; TW2
+// after TW1's N complex values.
+void build_twiddles_h(int r0, int r1, std::vector<_Float16>& t) {
+  const int N = r0 * r1;
+  std::vector<float> f;
+  build_twiddles(r0, r1, true, f);  // split layout: value v of (tile, lane) at float4 (tile*2 + v/2)*64 + lane
+  t.assign((size_t)2 * N * 2, (_Float16)0.f);
+  const int tiles = N / 256;
+  for (int part = 0; part < 2; part++)
+    for (int tile = 0; tile < tiles; tile++)
+      for (int lane = 0; lane < 64; lane++)
+        for (int v = 0; v < 4; v++) {
+          const float* src = &f[(size_t)part * 2 * N + (size_t)tw_index(true, tile, lane, v / 2) * 4 + 2 * (v % 2)];
+          _Float16* dst = &t[(size_t)part * 2 * N + ((size_t)tile * 64 + lane) * 8];
+          dst[v] = (_Float16)src[0];
+          dst[4 + v] = (_Float16)src[1];
+        }
+}
+
 std::mutex g_scratch_mu;
 void* g_scratch[256];  // per device: the device address of `scratch`
 
@@ -256,21 +276,28 @@ int scratch_for_device(void** out) {
 }
 
 std::mutex g_tw_mu;
-std::map<std::tuple<int, int, bool>, void*> g_tw[256];  // per device: (r0, r1, split) -> table
+std::map<std::tuple<int, int, int>, void*> g_tw[256];  // per device: (r0, r1, layout) -> table
 
-int device_twiddles(int r0, int r1, bool split, const void** out) {
+// Twiddle tables of plan r0 x r1 in `layout`: 0 paired (fp32), 1 split (fp32), 2 fp16.
+int device_twiddles(int r0, int r1, int layout, const void** out) {
   int dev = 0;
   hipError_t err = hipGetDevice(&dev);
   if (err != hipSuccess) return hip_status(err, "hipGetDevice");
   if (dev < 0 || dev >= 256) return SFFFT_EINVAL;
   std::lock_guard<std::mutex> lock(g_tw_mu);
-  void*& slot = g_tw[dev][std::make_tuple(r0, r1, split)];
+  void*& slot = g_tw[dev][std::make_tuple(r0, r1, layout)];
   if (!slot) {
-    std::vector<float> host;
-    build_twiddles(r0, r1, split, host);
+    std::vector<float> host32;
+    std::vector<_Float16> host16;
+    if (layout == 2)
+      build_twiddles_h(r0, r1, host16);
+    else
+      build_twiddles(r0, r1, layout == 1, host32);
+    const void* src = layout == 2 ? (const void*)host16.data() : (const void*)host32.data();
+    const size_t bytes = layout == 2 ? host16.size() * sizeof(_Float16) : host32.size() * sizeof(float);
     void* d = nullptr;
-    if ((err = hipMalloc(&d, host.size() * sizeof(float))) != hipSuccess) return hip_status(err, "hipMalloc");
-    if ((err = hipMemcpy(d, host.data(), host.size() * sizeof(float), hipMemcpyHostToDevice)) != hipSuccess) {
+    if ((err = hipMalloc(&d, bytes)) != hipSuccess) return hip_status(err, "hipMalloc");
+    if ((err = hipMemcpy(d, src, bytes, hipMemcpyHostToDevice)) != hipSuccess) {
       (void)hipFree(d);
       return hip_status(err, "hipMemcpy");
     }
@@ -436,7 +463,10 @@ int conv(const void* u, const void* kf, void* y, int B, int H, int L, const sfff
   const void* table = nullptr;
   if ((rc = device_table(&table))) return rc;
   const void* tw = nullptr;
-  if (e->mode == 1 && (rc = device_twiddles(p->r0, p->r1, tw_split(p->r0, p->r1), &tw))) return rc;
+  // wave plans: the fp16 tables for the fp16-products kernels (bf16 I/O or the
+  // fp16-accumulation mode, real filters), else the fp32 tables in the plan's layout
+  const bool hp = e->mode == 1 && !cplx && (IO == 1 || p->acc);
+  if (e->mode == 1 && (rc = device_twiddles(p->r0, p->r1, hp ? 2 : tw_split(p->r0, p->r1) ? 1 : 0, &tw))) return rc;
   const launch_fn fn = cplx && e->mode == 1 ? e->launch_complex[IO][p->cached] : e->launch[IO][p->cached];
   return hip_status(fn(u, kf, y, B, H, table, tw, p->acc, (hipStream_t)stream), "fused convolution launch");
 }
@@ -484,7 +514,7 @@ int conv_long(const void* u, const void* kf, void* y, void* work, size_t wbytes,
   const void* table = nullptr;
   if ((rc = device_table(&table))) return rc;
   const void* tw = nullptr;
-  if ((rc = device_twiddles(p->r1, p->r2, false, &tw))) return rc;
+  if ((rc = device_twiddles(p->r1, p->r2, 0, &tw))) return rc;
   return hip_status(e->launch[circ][IO](u, kf, y, work, B, H, chunk, table, tw, (hipStream_t)stream),
                     "multi-pass launch");
 }
@@ -897,12 +927,12 @@ int sffft_twiddle_probe(int N, const void* queries, int nq, int rows, float sc, 
   return hip_status(hipGetLastError(), "twiddle probe launch");
 }
 
-int sffft_twiddle_table(int r0, int r1, int split, void* out, size_t out_len) {
-  if (!valid_radix(r0) || !valid_radix(r1) || (split != 0 && split != 1) || !out) return SFFFT_EINVAL;
-  const size_t bytes = (size_t)r0 * r1 * 16;  // two tables of N complex fp32
+int sffft_twiddle_table(int r0, int r1, int layout, void* out, size_t out_len) {
+  if (!valid_radix(r0) || !valid_radix(r1) || layout < 0 || layout > 2 || !out) return SFFFT_EINVAL;
+  const size_t bytes = (size_t)r0 * r1 * (layout == 2 ? 8 : 16);  // two tables of N complex fp32 / fp16
   if (out_len < bytes) return SFFFT_EINVAL;
   const void* tw = nullptr;
-  const int rc = device_twiddles(r0, r1, split != 0, &tw);
+  const int rc = device_twiddles(r0, r1, layout, &tw);
   if (rc) return rc;
   return hip_status(hipMemcpy(out, tw, bytes, hipMemcpyDeviceToHost), "hipMemcpy");
 }

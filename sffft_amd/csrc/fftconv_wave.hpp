@@ -41,6 +41,14 @@
 // half the bytes, WavePlan::hs_index) and the lanes of columns k0 > R0/2 read the
 // partner frequency N-k and conjugate it; complex filters (HERM = false) read the
 // whole spectrum.
+//
+// fp16 products (HP: bf16 I/O and the fp16-accumulation mode, real filters): the two
+// twiddle tables hold fp16 values, [wr0..wr3 | wi0..wi3] per lane and tile (one 16-byte
+// read instead of two), and the twiddle products run in packed fp16 on accumulators
+// rounded to fp16 once (v_cvt_pk_f16_f32, v_pk_mul_f16, v_pk_fma_f16: 12 VALU
+// instructions per tile instead of 16). Each product then carries about three fp16
+// roundings instead of one, which bf16 I/O (8-bit output) and the fp16-accumulation
+// mode (which rounds every accumulator to fp16 anyway) leave within their error bounds.
 #pragma once
 #include "fftconv.hpp"
 
@@ -52,6 +60,8 @@
 namespace sffft {
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+typedef float f2 __attribute__((ext_vector_type(2)));
 
 template <int R0_, int R1_>
 struct WavePlan {
@@ -63,6 +73,9 @@ struct WavePlan {
   static constexpr int F0_H8 = ST * ST * 128;  // both fragment kinds
   static constexpr int F1_H8 = R1 == R0 ? 0 : MT * MT * 128;
   static constexpr int TW_F4 = N / 2;  // one twiddle table: N complex fp32 = N/2 float4
+  // one twiddle table in the table format of the kernel: fp32, or with fp16 products (hp)
+  // N complex fp16 = N/4 float4
+  static constexpr int twb_f4(bool hp) { return hp ? N / 4 : N / 2; }
   static constexpr int SP_F4 = N / 2;  // one channel's whole spectrum: N complex64 = N/2 float4
   // One channel's Hermitian half spectrum (hs_index): columns k0 = 0..R0/2 of HPITCH
   // float4 each (8*MT values and one of padding: an odd pitch puts the 16 columns a
@@ -73,26 +86,27 @@ struct WavePlan {
   // ch channels' spectra in LDS, in whole 64-float4 runs of the table copy
   static constexpr int spl_f4(int ch, bool herm) { return (ch * sp_f4(herm) + 63) / 64 * 64; }
   static constexpr int TW_TABLES = R0 == R1 ? 1 : 2;
-  static constexpr int TAB_F4 = F0_H8 + F1_H8 + TW_TABLES * TW_F4;
+  static constexpr int tab_f4(bool hp) { return F0_H8 + F1_H8 + TW_TABLES * twb_f4(hp); }
   // the same with the first fragment kind only (the second is derived in registers)
-  static constexpr int TAB1_F4 = (F0_H8 + F1_H8) / 2 + TW_TABLES * TW_F4;
+  static constexpr int tab1_f4(bool hp) { return (F0_H8 + F1_H8) / 2 + TW_TABLES * twb_f4(hp); }
   // per-wavefront operand scratch of the row loads with fp32 I/O (bf16 needs less)
   static constexpr int SCRATCH_MAX = 16 * (M + 4) * 4;
   // Layout for a workgroup of nw wavefronts serving ch channels, in order of preference:
   // both DFT fragment kinds and the spectra in LDS; the first kind only with the spectra
   // in LDS; the first kind only with the spectra read through L2. Every layout reads the
   // pairs as row chunks through the operand scratch.
-  static constexpr bool both_kinds(int ch, int nw, bool herm = true) {
-    return (TAB_F4 + spl_f4(ch, herm)) * 16 + nw * SCRATCH_MAX <= 163840;
+  // hp: the fp16 twiddle tables of the fp16-products kernels (half the bytes).
+  static constexpr bool both_kinds(int ch, int nw, bool herm = true, bool hp = false) {
+    return (tab_f4(hp) + spl_f4(ch, herm)) * 16 + nw * SCRATCH_MAX <= 163840;
   }
-  static constexpr int tables_f4(int ch, int nw, bool herm = true) {
-    return both_kinds(ch, nw, herm) ? TAB_F4 : TAB1_F4;
+  static constexpr int tables_f4(int ch, int nw, bool herm = true, bool hp = false) {
+    return both_kinds(ch, nw, herm, hp) ? tab_f4(hp) : tab1_f4(hp);
   }
-  static constexpr bool spectra_in_lds(int ch, int nw, bool herm = true) {
-    return (tables_f4(ch, nw, herm) + spl_f4(ch, herm)) * 16 + nw * SCRATCH_MAX <= 163840;
+  static constexpr bool spectra_in_lds(int ch, int nw, bool herm = true, bool hp = false) {
+    return (tables_f4(ch, nw, herm, hp) + spl_f4(ch, herm)) * 16 + nw * SCRATCH_MAX <= 163840;
   }
-  static constexpr int lds_bytes(int ch, int nw, bool herm = true) {
-    return (tables_f4(ch, nw, herm) + (spectra_in_lds(ch, nw, herm) ? spl_f4(ch, herm) : 0)) * 16 +
+  static constexpr int lds_bytes(int ch, int nw, bool herm = true, bool hp = false) {
+    return (tables_f4(ch, nw, herm, hp) + (spectra_in_lds(ch, nw, herm, hp) ? spl_f4(ch, herm) : 0)) * 16 +
            nw * SCRATCH_MAX;
   }
   static_assert(R0 >= 16 && R0 <= 64 && R1 >= 16 && R1 <= 64, "radices are 16, 32 or 64");
@@ -149,6 +163,20 @@ __device__ __forceinline__ h8 cmul_pack(f4 dr, f4 di, float4 w01, float4 w23) {
     o[4 + v] = (_Float16)(dr[v] * wi[v] + di[v] * wr[v]);
   }
   return o;
+}
+
+// The same in packed fp16 (fp16 products): the accumulators rounded to fp16 once, w from
+// the fp16 table as [wr0 wr1 wr2 wr3 | wi0 wi1 wi2 wi3], two packed products per pair of
+// values.
+__device__ __forceinline__ h8 cmul_pack_h(f4 dr, f4 di, h8 w) {
+  const h2 r01 = __builtin_convertvector((f2){dr[0], dr[1]}, h2);
+  const h2 r23 = __builtin_convertvector((f2){dr[2], dr[3]}, h2);
+  const h2 i01 = __builtin_convertvector((f2){di[0], di[1]}, h2);
+  const h2 i23 = __builtin_convertvector((f2){di[2], di[3]}, h2);
+  const h2 wr01 = {w[0], w[1]}, wr23 = {w[2], w[3]}, wi01 = {w[4], w[5]}, wi23 = {w[6], w[7]};
+  const h2 or01 = r01 * wr01 - i01 * wi01, or23 = r23 * wr23 - i23 * wi23;
+  const h2 oi01 = r01 * wi01 + i01 * wr01, oi23 = r23 * wi23 + i23 * wr23;
+  return (h8){or01[0], or01[1], or23[0], or23[1], oi01[0], oi01[1], oi23[0], oi23[1]};
 }
 
 // conj((dr + i di) * k) for four spectrum values k (float4 pairs of complex64); with
@@ -381,12 +409,22 @@ __device__ __forceinline__ void store_rows(TIO* S, const f4 (&z)[P::MT], TIO* __
 // Every stage of one pair, from its loaded operands to the stored outputs; SP is the
 // channel's spectrum in LDS. SPLIT: fp32 input as value plus remainder (pair_operands),
 // two MFMAs per phase-1 product into the same accumulator.
-template <class P, class TIO, bool ACC16, bool HOLD_F1, bool K1, bool HERM, bool SPLIT>
+template <class P, class TIO, bool ACC16, bool HOLD_F1, bool K1, bool HERM, bool SPLIT, bool HP>
 __device__ __forceinline__ void process_pair(const PairLoads<P, TIO>& d, TIO* S, const float4* SP,
                                              TIO* __restrict__ ya, TIO* __restrict__ yb, const h8* F0,
                                              const h8* F1, const float4* TW1, const float4* TW2, int lane) {
   constexpr int R0 = P::R0, M = P::M, MT = P::MT, ST = P::ST, KS1 = P::KS1, NT3 = P::NT3;
   constexpr bool TWS = tw_split(P::R0, P::R1);  // twiddle-table layout (tw_index)
+  // twiddled tile t of the table TW: fp32 table and products, or (HP) fp16 table and
+  // packed fp16 products, whose conversion to fp16 is the accumulator's rounding
+  auto twiddled = [&](const float4* TW, int t, f4 dr, f4 di) -> h8 {
+    if constexpr (HP) {
+      return cmul_pack_h(dr, di, reinterpret_cast<const h8*>(TW)[t * 64 + lane]);
+    } else {
+      return cmul_pack(acc_round<ACC16>(dr), acc_round<ACC16>(di), TW[tw_index(TWS, t, lane, 0)],
+                       TW[tw_index(TWS, t, lane, 1)]);
+    }
+  };
   // With 16 tiles per transform (64x64) the pair alone fills 64 VGPRs; compiler-only
   // barriers at the top of each tile step keep the next step's table and spectrum
   // loads from being hoisted over the current one, which would not fit beside it.
@@ -420,10 +458,7 @@ __device__ __forceinline__ void process_pair(const PairLoads<P, TIO>& d, TIO* S,
           di = mfma(alo[mt][ks], f1[ks], di);
         }
       }
-      dr = acc_round<ACC16>(dr);
-      di = acc_round<ACC16>(di);
-      const int t = mt * ST + nt;
-      b2[mt][nt] = cmul_pack(dr, di, TW1[tw_index(TWS, t, lane, 0)], TW1[tw_index(TWS, t, lane, 1)]);
+      b2[mt][nt] = twiddled(TW1, mt * ST + nt, dr, di);
     }
   }
 
@@ -492,9 +527,7 @@ __device__ __forceinline__ void process_pair(const PairLoads<P, TIO>& d, TIO* S,
       }
 #pragma unroll
       for (int j = 0; j < SG; j++) {
-        const int tt = (s0 + j) * MT + t;
-        b2[t][s0 + j] = cmul_pack(acc_round<ACC16>(er[j]), acc_round<ACC16>(ei[j]), TW2[tw_index(TWS, tt, lane, 0)],
-                                  TW2[tw_index(TWS, tt, lane, 1)]);
+        b2[t][s0 + j] = twiddled(TW2, (s0 + j) * MT + t, er[j], ei[j]);
       }
     }
   }
@@ -538,18 +571,25 @@ __global__ void __launch_bounds__(64 * NW)
     fftconv_wave_kernel(const TIO* __restrict__ u, const float4* __restrict__ kf, TIO* __restrict__ y, int B,
                         int H, const h8* __restrict__ ftab, const float4* __restrict__ twtab) {
   constexpr int R0 = P::R0;
-  constexpr bool K1 = !P::both_kinds(CH, NW, HERM);  // first DFT fragment kind only
+  // fp16 products: bf16 I/O and the fp16-accumulation mode (real filters)
+  constexpr bool HP = HERM && (sizeof(TIO) == 2 || ACC16);
+#ifdef SFFFT_WAVE_FORCE_K1
+  constexpr bool K1 = true;
+#else
+  constexpr bool K1 = !P::both_kinds(CH, NW, HERM, HP);  // first DFT fragment kind only
+#endif
   constexpr int SCR_F4 = scratch_bytes<P, TIO>() / 16;
-  constexpr bool SP_LDS = P::spectra_in_lds(CH, NW, HERM);
+  constexpr bool SP_LDS = P::spectra_in_lds(CH, NW, HERM, HP);
   constexpr int SPC_F4 = P::sp_f4(HERM);  // one channel's spectrum
-  constexpr int SPL_F4 = SP_LDS ? P::spl_f4(CH, HERM) : 0, TAB_F4 = P::tables_f4(CH, NW, HERM);
+  constexpr int SPL_F4 = SP_LDS ? P::spl_f4(CH, HERM) : 0;
+  constexpr int TAB_F4 = K1 ? P::tab1_f4(HP) : P::tab_f4(HP), TWB_F4 = P::twb_f4(HP);
   constexpr int F0_H8 = K1 ? P::F0_H8 / 2 : P::F0_H8, F1_H8 = K1 ? P::F1_H8 / 2 : P::F1_H8;
-  static_assert((TAB_F4 + SPL_F4 + NW * SCR_F4) * 16 <= P::lds_bytes(CH, NW, HERM), "layout within the plan's LDS");
+  static_assert((TAB_F4 + SPL_F4 + NW * SCR_F4) * 16 <= 163840, "layout within the LDS of a CU");
   __shared__ float4 lds[TAB_F4 + SPL_F4 + NW * SCR_F4];
   h8* F0 = reinterpret_cast<h8*>(lds);
   h8* F1 = P::R1 == P::R0 ? F0 : F0 + F0_H8;
   float4* TW1 = lds + F0_H8 + F1_H8;
-  float4* TW2 = P::TW_TABLES == 2 ? TW1 + P::TW_F4 : TW1;
+  float4* TW2 = P::TW_TABLES == 2 ? TW1 + TWB_F4 : TW1;
   float4* SPL = lds + TAB_F4;
 
   // the wavefront index is uniform: read it into a scalar register so the pair and
@@ -560,7 +600,7 @@ __global__ void __launch_bounds__(64 * NW)
   const int nch = H - h0 < CH ? H - h0 : CH;  // channels of this workgroup
 
   // ---- tables and spectra: direct global -> LDS copies, issued first
-  dma_to_lds<P::TW_TABLES * P::TW_F4, NW>(TW1, [&](int k) { return twtab + k; }, lane, wave);
+  dma_to_lds<P::TW_TABLES * TWB_F4, NW>(TW1, [&](int k) { return twtab + k; }, lane, wave);
   if constexpr (CACHED) {
     // with K1 the first-kind runs only: LDS run i is table run 2i
     auto tab = [&](int R, int k) {
@@ -638,7 +678,7 @@ __global__ void __launch_bounds__(64 * NW)
   if (wave < npairs) {
     const int c = wave / BP, bp = wave - c * BP;
     const size_t ra = ((size_t)(2 * bp) * H + h0 + c) * P::L, rb = ra + (size_t)H * P::L;
-    process_pair<P, TIO, ACC16, HOLD, K1, HERM, SPLIT>(cur, S, spec(c), y + ra, y + rb, F0, F1, TW1, TW2, lane);
+    process_pair<P, TIO, ACC16, HOLD, K1, HERM, SPLIT, HP>(cur, S, spec(c), y + ra, y + rb, F0, F1, TW1, TW2, lane);
   }
   for (int p = wave + NW; p < npairs; p += NW) {
     // compiler-only barrier: keeps the table reads inside the loop (hoisting them
@@ -652,7 +692,7 @@ __global__ void __launch_bounds__(64 * NW)
     const int c = p / BP, bp = p - c * BP;
     const size_t ra = ((size_t)(2 * bp) * H + h0 + c) * P::L, rb = ra + (size_t)H * P::L;
     issue_pair_loads<P, TIO>(u + ra, u + rb, cur, ln);
-    process_pair<P, TIO, ACC16, HOLD, K1, HERM, SPLIT>(cur, S, spec(c), y + ra, y + rb, F0, F1, TW1, TW2, ln);
+    process_pair<P, TIO, ACC16, HOLD, K1, HERM, SPLIT, HP>(cur, S, spec(c), y + ra, y + rb, F0, F1, TW1, TW2, ln);
   }
 }
 

@@ -2,7 +2,8 @@
 w^e = exp(-2 pi i e / N) with e the product of an index and a frequency digit.
 
 - The wave pipeline's fp32 tables (built in fp64 on the host, read back through
-  sffft_twiddle_table). Every entry of TW1 = sc0 w^(m k0) and TW2 = sc0 sc1 w^(k0 n1) at its
+  sffft_twiddle_table), and their fp16 form for the fp16-products kernels (within half an
+  fp16 ulp). Every entry of TW1 = sc0 w^(m k0) and TW2 = sc0 sc1 w^(k0 n1) at its
   slot of the documented layout (tile, lane (c, g), value v; m = 16 mt + 4 g + v,
   k0 = 16 nt + c for TW1, k0 = 16 s + 4 g + v, n1 = 16 t + c for TW2), against numpy's fp64
   cos/sin of the exact angle: within one fp32 rounding, |err| <= 2^-24 |w|.
@@ -67,6 +68,17 @@ def _unpack(raw, ntiles, split):
     return out
 
 
+def _unpack_h(raw, ntiles):
+    """fp16 table (layout 2): h8 per (tile, lane) = [wr0..wr3 | wi0..wi3]."""
+    h = raw.reshape(ntiles, 64, 8).astype(np.float64)
+    return h[..., :4] + 1j * h[..., 4:]
+
+
+def _fp16_rounding_ok(got, want):
+    tol = 2.0 ** -11 * np.abs(want) * (1 + 1e-6) + 2.0 ** -25  # half an ulp, subnormals included
+    return bool(np.all(np.abs(got.real - want.real) <= tol) and np.all(np.abs(got.imag - want.imag) <= tol))
+
+
 def _fp32_rounding_ok(got, want):
     tol = 2.0 ** -24 * np.abs(want) * (1 + 1e-6) + 1e-30
     return bool(np.all(np.abs(got.real - want.real) <= tol) and np.all(np.abs(got.imag - want.imag) <= tol))
@@ -90,7 +102,7 @@ def _table_plans():
 def test_wave_twiddle_tables(r0, r1, split):
     N = r0 * r1
     raw = np.zeros(N * 4, np.float32)
-    rc = sf.lib().sffft_twiddle_table(r0, r1, int(split), raw.ctypes.data_as(ctypes.c_void_p), raw.nbytes)
+    rc = sf.lib().sffft_twiddle_table(r0, r1, 1 if split else 0, raw.ctypes.data_as(ctypes.c_void_p), raw.nbytes)
     assert rc == sf.SFFFT_OK, sf.strerror(rc)
     ntiles = (r0 // 16) * (r1 // 16)
     got1 = _unpack(raw[:2 * N], ntiles, split)
@@ -102,6 +114,24 @@ def test_wave_twiddle_tables(r0, r1, split):
     # planted mistakes in the reference fail the same check
     assert not _fp32_rounding_ok(got1, np.conj(want1))
     assert not _fp32_rounding_ok(got1, want1 * np.exp(-2j * np.pi / N))  # exponent one step off
+
+
+@pytest.mark.parametrize("r0,r1", sorted({(r0, r1) for r0, r1, split in _table_plans() if split or r0 == r1 == 64}))
+def test_wave_twiddle_tables_fp16(r0, r1):
+    """The fp16 tables of the fp16-products wave kernels (bf16 I/O, fp16 accumulation): the
+    same values rounded to fp16, within half an fp16 ulp of the fp64 definition."""
+    N = r0 * r1
+    raw = np.zeros(N * 4, np.float16)
+    rc = sf.lib().sffft_twiddle_table(r0, r1, 2, raw.ctypes.data_as(ctypes.c_void_p), raw.nbytes)
+    assert rc == sf.SFFFT_OK, sf.strerror(rc)
+    ntiles = (r0 // 16) * (r1 // 16)
+    got1, got2 = _unpack_h(raw[:2 * N], ntiles), _unpack_h(raw[2 * N:], ntiles)
+    want1, want2 = _wave_reference(r0, r1)
+    print(f"fp16 twiddle table {r0}x{r1}: max |err| {max(np.abs(got1 - want1).max(), np.abs(got2 - want2).max()):.2e}",
+          flush=True)
+    assert _fp16_rounding_ok(got1, want1) and _fp16_rounding_ok(got2, want2), (r0, r1)
+    assert not _fp16_rounding_ok(got1, np.conj(want1))
+    assert not _fp16_rounding_ok(got1, want1 * np.exp(-2j * np.pi / N))
 
 
 def _probe(dev, N, q, sc):
