@@ -245,8 +245,7 @@ int sffft_dft_table(void* out, size_t out_len);
  * N a power of two in [256, 32768]. sffft_twiddle_table copies the wave pipeline's twiddle
  * tables of plan r0 x r1 (built in fp64 on the host) to host memory `out`: layout 1 = fp32
  * split (the wave kernels'), 0 = fp32 paired (64x64 and the multi-pass row pass), r0*r1*16
- * bytes; 2 = fp16 (the fp16-products wave kernels of bf16 I/O and fp16 accumulation),
- * r0*r1*8 bytes. */
+ * bytes; 2 = fp16 (the wave kernels of the fp16-accumulation mode), r0*r1*8 bytes. */
 int sffft_twiddle_probe(int N, const void* queries, int nq, int rows, float sc, void* out, void* stream);
 int sffft_twiddle_table(int r0, int r1, int layout, void* out, size_t out_len);
 

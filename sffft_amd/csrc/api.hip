@@ -463,9 +463,9 @@ int conv(const void* u, const void* kf, void* y, int B, int H, int L, const sfff
   const void* table = nullptr;
   if ((rc = device_table(&table))) return rc;
   const void* tw = nullptr;
-  // wave plans: the fp16 tables for the fp16-products kernels (bf16 I/O or the
-  // fp16-accumulation mode, real filters), else the fp32 tables in the plan's layout
-  const bool hp = e->mode == 1 && !cplx && (IO == 1 || p->acc);
+  // wave plans: the fp16 tables for the fp16-products kernels (the fp16-accumulation
+  // mode, real filters), else the fp32 tables in the plan's layout
+  const bool hp = e->mode == 1 && !cplx && p->acc;
   if (e->mode == 1 && (rc = device_twiddles(p->r0, p->r1, hp ? 2 : tw_split(p->r0, p->r1) ? 1 : 0, &tw))) return rc;
   const launch_fn fn = cplx && e->mode == 1 ? e->launch_complex[IO][p->cached] : e->launch[IO][p->cached];
   return hip_status(fn(u, kf, y, B, H, table, tw, p->acc, (hipStream_t)stream), "fused convolution launch");

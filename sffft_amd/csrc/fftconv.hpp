@@ -40,6 +40,8 @@
 //    remainder (SFFFT_FP32_SPLITS), removing the largest rounding term.
 #pragma once
 #include <hip/hip_runtime.h>
+
+#include <type_traits>
 #include <stdint.h>
 
 // fp16 operands of fp32-I/O three-stage plans that also carry their fp16 remainder
@@ -274,6 +276,43 @@ __device__ __forceinline__ h4 to_h4(const float* x) {
   return (h4){(_Float16)x[0], (_Float16)x[1], (_Float16)x[2], (_Float16)x[3]};
 }
 
+// ---- Products of the fp16-accumulation mode -------------------------------------
+// The mode rounds every accumulator to fp16 (the reference's fp16 accumulators,
+// src/sffft.cu:88,397-398). Its twiddle and spectrum products then run in packed fp16 on
+// those rounded values: v_cvt_pk_f16_f32 (the rounding itself), v_pk_mul_f16 and
+// v_pk_fma_f16, two values per instruction, instead of the fp32 products and separate
+// roundings of fp32 accumulation: the speed-for-precision trade of that mode
+// (README.md:112-122).
+typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+typedef float f2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ h2 pk_h2(float a, float b) { return __builtin_convertvector((f2){a, b}, h2); }
+// four complex factors in packed fp16
+struct HW {
+  h2 r01, r23, i01, i23;
+};
+__device__ __forceinline__ HW hw_of(const float* wr, const float* wi) {
+  return HW{pk_h2(wr[0], wr[1]), pk_h2(wr[2], wr[3]), pk_h2(wi[0], wi[1]), pk_h2(wi[2], wi[3])};
+}
+// (dr + i di) w for four values, as fp16 real parts xr and imaginary parts xi (CONJ: the
+// conjugate of the product)
+template <bool CONJ = false>
+__device__ __forceinline__ void cmul_hp(f4 dr, f4 di, const HW& w, h4& xr, h4& xi) {
+  const h2 r01 = pk_h2(dr[0], dr[1]), r23 = pk_h2(dr[2], dr[3]);
+  const h2 i01 = pk_h2(di[0], di[1]), i23 = pk_h2(di[2], di[3]);
+  const h2 a = r01 * w.r01 - i01 * w.i01, b = r23 * w.r23 - i23 * w.i23;
+  h2 c, d;
+  if constexpr (CONJ) {
+    c = -(r01 * w.i01) - i01 * w.r01;
+    d = -(r23 * w.i23) - i23 * w.r23;
+  } else {
+    c = r01 * w.i01 + i01 * w.r01;
+    d = r23 * w.i23 + i23 * w.r23;
+  }
+  xr = (h4){a[0], a[1], b[0], b[1]};
+  xi = (h4){c[0], c[1], d[0], d[1]};
+}
+__device__ __forceinline__ h8 join_h8(h4 a, h4 b) { return (h8){a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]}; }
+
 // ---- Phase 1: first forward stage over n0 (src/sffft.cu:266-274) ---------------
 // Input rows are natural order, n = n0*M + m. Data is the A operand (M = 16
 // consecutive m, K = n0); only n0 < R0/2 is loaded (the zero-padded half is
@@ -421,25 +460,31 @@ __device__ __forceinline__ void phase1(const P1Data<P, NW, NSEQ, TIO>& d, P1Frag
             dr = mfma(a[ks][p], frag(j, nt, ks, 0), dr);
             di = mfma(a[ks][p], frag(j, nt, ks, 1), di);
           }
-        dr = round_acc(dr, acc16);
-        di = round_acc(di, acc16);
         const int k0 = 16 * nt + r;
-        float wr[4], wi[4], xr[4], xi[4];
+        float wr[4], wi[4];
         if (PF > 0 && i == 0) {
 #pragma unroll
           for (int v = 0; v < 4; v++) wr[v] = t0r[PF > 0 ? j : 0][v], wi[v] = t0i[PF > 0 ? j : 0][v];
         } else {
           twiddle4<N>(k0, 16 * mt + 4 * g, sc0, wr, wi);
         }
+        h4 hr, hi;  // the twiddled tile in fp16
+        if (acc16) {
+          cmul_hp(dr, di, hw_of(wr, wi), hr, hi);
+        } else {
+          float xr[4], xi[4];
 #pragma unroll
-        for (int v = 0; v < 4; v++) {
-          xr[v] = dr[v] * wr[v] - di[v] * wi[v];
-          xi[v] = dr[v] * wi[v] + di[v] * wr[v];
+          for (int v = 0; v < 4; v++) {
+            xr[v] = dr[v] * wr[v] - di[v] * wi[v];
+            xi[v] = dr[v] * wi[v] + di[v] * wr[v];
+          }
+          hr = to_h4(xr);
+          hi = to_h4(xi);
         }
         if constexpr (P::S == 2) {
           const int pos = k0 * P::PA + 16 * mt + 4 * g;  // [k0][n1]
-          *reinterpret_cast<h4*>(re + pos) = to_h4(xr);
-          *reinterpret_cast<h4*>(im + pos) = to_h4(xi);
+          *reinterpret_cast<h4*>(re + pos) = hr;
+          *reinterpret_cast<h4*>(im + pos) = hi;
         } else {
 #pragma unroll
           for (int v = 0; v < 4; v++) {  // [k0][n2 ^ (k0 & 15)][n1]
@@ -448,8 +493,8 @@ __device__ __forceinline__ void phase1(const P1Data<P, NW, NSEQ, TIO>& d, P1Frag
             // them over 16 rows and banks. phase2_s3 reads the row back swizzled.
             const int m = 16 * mt + 4 * g + v, n1 = m / P::R2, n2 = m % P::R2;
             const int pos = k0 * P::ROW + (n2 ^ (k0 & 15)) * P::PA + n1;
-            re[pos] = (_Float16)xr[v];
-            im[pos] = (_Float16)xi[v];
+            re[pos] = hr[v];
+            im[pos] = hi[v];
           }
         }
       }
@@ -471,14 +516,22 @@ __device__ __forceinline__ void load_k4(const float2* __restrict__ kp, int lane,
 // follows runs on hi and on lo (twice the MFMAs of that stage), so the product enters
 // it with about 22 significant bits instead of 11. One fp16 rounding of the five of a
 // three-stage plan (three of a two-stage one) is removed this way.
+// With acc16 (the fp16-accumulation mode) the raw accumulators are given and the product
+// runs in packed fp16 (cmul_hp).
 template <int T, bool SPLIT = false>
 __device__ __forceinline__ void spectrum_product(const f4* dr, const f4* di, const float4 (*q)[2], h8* a2,
-                                                 h8* lo = nullptr) {
+                                                 h8* lo = nullptr, int acc16 = 0) {
 #pragma unroll
   for (int mt = 0; mt < T; mt++) {
     const float4 k01 = q[mt][0], k23 = q[mt][1];
     const float kr[4] = {k01.x, k01.z, k23.x, k23.z};
     const float ki[4] = {k01.y, k01.w, k23.y, k23.w};
+    if (acc16) {
+      h4 hr, hi;
+      cmul_hp<true>(dr[mt], di[mt], hw_of(kr, ki), hr, hi);
+      a2[mt] = join_h8(hr, hi);
+      continue;
+    }
 #pragma unroll
     for (int v = 0; v < 4; v++) {
       const float xr = dr[mt][v] * kr[v] - di[mt][v] * ki[v];
@@ -539,11 +592,9 @@ __device__ __forceinline__ void phase2_s2(_Float16* re, _Float16* im, const KDat
           dr[mt] = mfma(cf_frag<R1, CACHED>(ftab, mt, ks, 0, lane), b[ks], dr[mt]);
           di[mt] = mfma(cf_frag<R1, CACHED>(ftab, mt, ks, 1, lane), b[ks], di[mt]);
         }
-        dr[mt] = round_acc(dr[mt], acc16);
-        di[mt] = round_acc(di[mt], acc16);
       }
       h8 a2[T1], a2lo[SPLIT ? T1 : 1];
-      spectrum_product<T1, SPLIT>(dr, di, kd.q[i], a2, a2lo);
+      spectrum_product<T1, SPLIT>(dr, di, kd.q[i], a2, a2lo, acc16);
 #pragma unroll
       for (int nt = 0; nt < T1; nt++) {
         f4 er = {0.f, 0.f, 0.f, 0.f}, ei = {0.f, 0.f, 0.f, 0.f};
@@ -556,17 +607,20 @@ __device__ __forceinline__ void phase2_s2(_Float16* re, _Float16* im, const KDat
             ei = mfma(a2lo[mt], cf_frag<R1, CACHED>(ftab, nt, mt, 1, lane), ei);
           }
         }
-        er = round_acc(er, acc16);
-        ei = round_acc(ei, acc16);
-        float wr[4], wi[4], xr[4], xi[4];
+        float wr[4], wi[4];
         twiddle4<N>(16 * nt + c, 16 * s + 4 * g, sc1, wr, wi);
+        if (acc16) {
+          cmul_hp(er, ei, hw_of(wr, wi), outr[i][nt], outi[i][nt]);
+        } else {
+          float xr[4], xi[4];
 #pragma unroll
-        for (int v = 0; v < 4; v++) {
-          xr[v] = er[v] * wr[v] - ei[v] * wi[v];
-          xi[v] = er[v] * wi[v] + ei[v] * wr[v];
+          for (int v = 0; v < 4; v++) {
+            xr[v] = er[v] * wr[v] - ei[v] * wi[v];
+            xi[v] = er[v] * wi[v] + ei[v] * wr[v];
+          }
+          outr[i][nt] = to_h4(xr);
+          outi[i][nt] = to_h4(xi);
         }
-        outr[i][nt] = to_h4(xr);
-        outi[i][nt] = to_h4(xi);
       }
     }
   }
@@ -663,6 +717,36 @@ __device__ __forceinline__ void phase2_s3(_Float16* re, _Float16* im, const floa
       xi[v] = er[v] * wi[v] + ei[v] * wr[v];
     }
   };
+  // the twiddled accumulators as an fp16 operand (with its remainder when `split`); in the
+  // fp16-accumulation mode the packed fp16 product of the raw accumulators
+  auto twiddle_pack = [&](const f4& er, const f4& ei, const float* wr, const float* wi, h8& hi, h8& lo,
+                          auto split) {
+    if (acc16) {
+      h4 a, b;
+      cmul_hp(er, ei, hw_of(wr, wi), a, b);
+      hi = join_h8(a, b);
+    } else {
+      float xr[4], xi[4];
+      twiddle(er, ei, wr, wi, xr, xi);
+      pack_operand<decltype(split)::value>(xr, xi, hi, lo);
+    }
+  };
+  // the last twiddle of a row tile, stored as fp16 into the row's block at pos
+  auto twiddle_store = [&](const f4& zr, const f4& zi, const float* wr, const float* wi, int pos) {
+    h4 hr, hi;
+    if (acc16) {
+      cmul_hp(zr, zi, hw_of(wr, wi), hr, hi);
+    } else {
+      float xr[4], xi[4];
+      twiddle(zr, zi, wr, wi, xr, xi);
+      hr = to_h4(xr);
+      hi = to_h4(xi);
+    }
+    *reinterpret_cast<h4*>(re + pos) = hr;
+    *reinterpret_cast<h4*>(im + pos) = hi;
+  };
+  using SBT = std::integral_constant<bool, SB != 0>;
+  using SET = std::integral_constant<bool, SE != 0>;
   // A row's spectrum (kernel order, 2 KB per tile) is read from L2 while the row
   // before it is computed: with one tile per axis the loads are issued one row ahead
   // (double-buffered); otherwise at the start of their own row, in flight while the
@@ -727,12 +811,9 @@ __device__ __forceinline__ void phase2_s3(_Float16* re, _Float16* im, const floa
               dr = mfma(a[t2][ks], f1(nt, ks, 0), dr);
               di = mfma(a[t2][ks], f1(nt, ks, 1), di);
             }
-            dr = round_acc(dr, acc16);
-            di = round_acc(di, acc16);
-            float wr[4], wi[4], xr[4], xi[4];
+            float wr[4], wi[4];
             tw_n1(nt, t2, sc1, wr, wi);
-            twiddle(dr, di, wr, wi, xr, xi);
-            pack_operand<SB != 0>(xr, xi, b[nt][t2][0], b[nt][t2][SB]);
+            twiddle_pack(dr, di, wr, wi, b[nt][t2][0], b[nt][t2][SB], SBT{});
           }
         }
       }
@@ -752,11 +833,9 @@ __device__ __forceinline__ void phase2_s3(_Float16* re, _Float16* im, const floa
               dr[mt] = mfma(f2(mt, ks, 0), b[t1][ks][p], dr[mt]);
               di[mt] = mfma(f2(mt, ks, 1), b[t1][ks][p], di[mt]);
             }
-          dr[mt] = round_acc(dr[mt], acc16);
-          di[mt] = round_acc(di[mt], acc16);
         }
         h8 a2[T2], a2lo[SA ? T2 : 1];
-        spectrum_product<T2, SA>(dr, di, kq[KQB == 2 ? i & 1 : 0][t1], a2, a2lo);
+        spectrum_product<T2, SA>(dr, di, kq[KQB == 2 ? i & 1 : 0][t1], a2, a2lo, acc16);
 #pragma unroll
         for (int nt = 0; nt < T2; nt++) {
           f4 er = {0.f, 0.f, 0.f, 0.f}, ei = {0.f, 0.f, 0.f, 0.f};
@@ -769,12 +848,9 @@ __device__ __forceinline__ void phase2_s3(_Float16* re, _Float16* im, const floa
               ei = mfma(a2lo[mt], f2(nt, mt, 1), ei);
             }
           }
-          er = round_acc(er, acc16);
-          ei = round_acc(ei, acc16);
-          float wr[4], wi[4], xr[4], xi[4];
+          float wr[4], wi[4];
           tw_n1(nt, t1, sc2, wr, wi);
-          twiddle(er, ei, wr, wi, xr, xi);
-          pack_operand<SE != 0>(xr, xi, e[nt][t1][0], e[nt][t1][SE]);
+          twiddle_pack(er, ei, wr, wi, e[nt][t1][0], e[nt][t1][SE], SET{});
         }
       }
       // inverse over k1 and the last twiddle
@@ -791,10 +867,8 @@ __device__ __forceinline__ void phase2_s3(_Float16* re, _Float16* im, const floa
               zr = mfma(f1(mt, ks, 0), e[nt][ks][p], zr);
               zi = mfma(f1(mt, ks, 1), e[nt][ks][p], zi);
             }
-          zr = round_acc(zr, acc16);
-          zi = round_acc(zi, acc16);
           // lane value v is n1 = 16mt + 4g + v, n2 = 16nt + c: m = n1 R2 + n2
-          float wr[4], wi[4], xr[4], xi[4];
+          float wr[4], wi[4];
           if constexpr (REC) {
 #pragma unroll
             for (int v = 0; v < 4; v++) wr[v] = lr[v], wi[v] = li[v];
@@ -802,12 +876,9 @@ __device__ __forceinline__ void phase2_s3(_Float16* re, _Float16* im, const floa
           } else {
             twiddle4e<N>(k0 * ((16 * mt + 4 * g) * R2 + 16 * nt + c), k0 * R2, sc1, wr, wi);
           }
-          twiddle(zr, zi, wr, wi, xr, xi);
           // back into the row's own block, [n2][n1]: only this wavefront reads the row,
           // and all of its input is in registers by now
-          const int pos = rb + (16 * nt + c) * P::PA + 16 * mt + 4 * g;
-          *reinterpret_cast<h4*>(re + pos) = to_h4(xr);
-          *reinterpret_cast<h4*>(im + pos) = to_h4(xi);
+          twiddle_store(zr, zi, wr, wi, rb + (16 * nt + c) * P::PA + 16 * mt + 4 * g);
         }
       }
     }
@@ -851,12 +922,9 @@ __device__ __forceinline__ void phase2_s3(_Float16* re, _Float16* im, const floa
                 dr = mfma(a[u][t2][ks], f1(nt, ks, 0), dr);
                 di = mfma(a[u][t2][ks], f1(nt, ks, 1), di);
               }
-              dr = round_acc(dr, acc16);
-              di = round_acc(di, acc16);
-              float wr[4], wi[4], xr[4], xi[4];
+              float wr[4], wi[4];
               tw_n1(nt, t2, sc1, wr, wi);
-              twiddle(dr, di, wr, wi, xr, xi);
-              pack_operand<SB != 0>(xr, xi, b[u][nt][t2][0], b[u][nt][t2][SB]);
+              twiddle_pack(dr, di, wr, wi, b[u][nt][t2][0], b[u][nt][t2][SB], SBT{});
             }
           }
         }
@@ -879,11 +947,9 @@ __device__ __forceinline__ void phase2_s3(_Float16* re, _Float16* im, const floa
                 dr[mt] = mfma(f2(mt, ks, 0), b[u][t1][ks][p], dr[mt]);
                 di[mt] = mfma(f2(mt, ks, 1), b[u][t1][ks][p], di[mt]);
               }
-            dr[mt] = round_acc(dr[mt], acc16);
-            di[mt] = round_acc(di[mt], acc16);
           }
           h8 a2[T2], a2lo[SA ? T2 : 1];
-          spectrum_product<T2, SA>(dr, di, kq[u][t1], a2, a2lo);
+          spectrum_product<T2, SA>(dr, di, kq[u][t1], a2, a2lo, acc16);
 #pragma unroll
           for (int nt = 0; nt < T2; nt++) {
             f4 er = {0.f, 0.f, 0.f, 0.f}, ei = {0.f, 0.f, 0.f, 0.f};
@@ -896,12 +962,9 @@ __device__ __forceinline__ void phase2_s3(_Float16* re, _Float16* im, const floa
                 ei = mfma(a2lo[mt], f2(nt, mt, 1), ei);
               }
             }
-            er = round_acc(er, acc16);
-            ei = round_acc(ei, acc16);
-            float wr[4], wi[4], xr[4], xi[4];
+            float wr[4], wi[4];
             tw_n1(nt, t1, sc2, wr, wi);
-            twiddle(er, ei, wr, wi, xr, xi);
-            pack_operand<SE != 0>(xr, xi, e[u][nt][t1][0], e[u][nt][t1][SE]);
+            twiddle_pack(er, ei, wr, wi, e[u][nt][t1][0], e[u][nt][t1][SE], SET{});
           }
         }
       }
@@ -921,10 +984,8 @@ __device__ __forceinline__ void phase2_s3(_Float16* re, _Float16* im, const floa
                 zr = mfma(f1(mt, ks, 0), e[u][nt][ks][p], zr);
                 zi = mfma(f1(mt, ks, 1), e[u][nt][ks][p], zi);
               }
-            zr = round_acc(zr, acc16);
-            zi = round_acc(zi, acc16);
             // lane value v is n1 = 16mt + 4g + v, n2 = 16nt + c: m = n1 R2 + n2
-            float wr[4], wi[4], xr[4], xi[4];
+            float wr[4], wi[4];
             if constexpr (REC) {
 #pragma unroll
               for (int v = 0; v < 4; v++) wr[v] = lr[v], wi[v] = li[v];
@@ -932,12 +993,9 @@ __device__ __forceinline__ void phase2_s3(_Float16* re, _Float16* im, const floa
             } else {
               twiddle4e<N>(k0[u] * ((16 * mt + 4 * g) * R2 + 16 * nt + c), k0[u] * R2, sc1, wr, wi);
             }
-            twiddle(zr, zi, wr, wi, xr, xi);
             // back into the row's own block, [n2][n1]: only this wavefront reads the row,
             // and all of its input is in registers by now
-            const int pos = rb[u] + (16 * nt + c) * P::PA + 16 * mt + 4 * g;
-            *reinterpret_cast<h4*>(re + pos) = to_h4(xr);
-            *reinterpret_cast<h4*>(im + pos) = to_h4(xi);
+            twiddle_store(zr, zi, wr, wi, rb[u] + (16 * nt + c) * P::PA + 16 * mt + 4 * g);
           }
         }
       }
@@ -1061,6 +1119,9 @@ __global__ void __launch_bounds__(64 * NW, WPE)
   const size_t row_a = ((size_t)(bp * NSEQ) * H + h) * P::L;
   const size_t row_b = NSEQ == 2 ? row_a + (size_t)H * P::L : row_a;
   const float2* K = kf + (size_t)h * P::N;
+  // fp32 input as fp16 value plus remainder (fp32 accumulation; the fp16-accumulation mode
+  // keeps its one rounding)
+  constexpr bool SPLIT_IN = sizeof(TIO) == 4 && !ACC16 && (SFFFT_FP32_SPLITS & 8);
   // every global load of the input (and, for two-stage plans, of the spectrum) is
   // issued before any computation, so their latencies overlap
   P1Frags<P, NW, NSEQ, CACHED> fr;
@@ -1070,15 +1131,13 @@ __global__ void __launch_bounds__(64 * NW, WPE)
   if constexpr (P::S == 2) {
     KData2<P, NW> kd;
     k_prefetch_s2<P, NW>(K, kd, lane, wave);
-    phase1<P, NW, NSEQ, TIO, CACHED, sizeof(TIO) == 4 && (SFFFT_FP32_SPLITS & 8)>(ad, fr, re, im, ftab, acc16, lane,
-                                                                                   wave);
+    phase1<P, NW, NSEQ, TIO, CACHED, SPLIT_IN>(ad, fr, re, im, ftab, acc16, lane, wave);
     __syncthreads();
-    phase2_s2<P, NW, CACHED, sizeof(TIO) == 4>(re, im, kd, ftab, acc16, lane, wave);
+    phase2_s2<P, NW, CACHED, sizeof(TIO) == 4 && !ACC16>(re, im, kd, ftab, acc16, lane, wave);
   } else {
-    phase1<P, NW, NSEQ, TIO, CACHED, sizeof(TIO) == 4 && (SFFFT_FP32_SPLITS & 8)>(ad, fr, re, im, ftab, acc16, lane,
-                                                                                   wave);
+    phase1<P, NW, NSEQ, TIO, CACHED, SPLIT_IN>(ad, fr, re, im, ftab, acc16, lane, wave);
     __syncthreads();
-    phase2_s3<P, NW, CACHED, sizeof(TIO) == 4 ? SFFFT_FP32_SPLITS : 0>(re, im, K, ftab, acc16, lane, wave);
+    phase2_s3<P, NW, CACHED, sizeof(TIO) == 4 && !ACC16 ? SFFFT_FP32_SPLITS : 0>(re, im, K, ftab, acc16, lane, wave);
   }
   __syncthreads();
   phase3<P, NW, NSEQ, TIO, CACHED>(y + row_a, y + row_b, re, im, ftab, acc16, lane, wave);

@@ -42,13 +42,13 @@
 // partner frequency N-k and conjugate it; complex filters (HERM = false) read the
 // whole spectrum.
 //
-// fp16 products (HP: bf16 I/O and the fp16-accumulation mode, real filters): the two
-// twiddle tables hold fp16 values, [wr0..wr3 | wi0..wi3] per lane and tile (one 16-byte
-// read instead of two), and the twiddle products run in packed fp16 on accumulators
-// rounded to fp16 once (v_cvt_pk_f16_f32, v_pk_mul_f16, v_pk_fma_f16: 12 VALU
-// instructions per tile instead of 16). Each product then carries about three fp16
-// roundings instead of one, which bf16 I/O (8-bit output) and the fp16-accumulation
-// mode (which rounds every accumulator to fp16 anyway) leave within their error bounds.
+// fp16 products (HP: the fp16-accumulation mode, real filters): the two twiddle tables
+// hold fp16 values, [wr0..wr3 | wi0..wi3] per lane and tile (one 16-byte read instead of
+// two), and the twiddle products run in packed fp16 on the accumulators rounded to fp16
+// (v_cvt_pk_f16_f32, v_pk_mul_f16, v_pk_fma_f16: 12 VALU instructions per tile instead of
+// 16, the mode's accumulator rounding included). Each product then carries about three
+// fp16 roundings instead of one: the speed-for-precision trade of the reference's fp16
+// accumulation (README.md:112-122). fp32 accumulation keeps fp32 twiddles and products.
 #pragma once
 #include "fftconv.hpp"
 
@@ -60,8 +60,6 @@
 namespace sffft {
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-typedef _Float16 h2 __attribute__((ext_vector_type(2)));
-typedef float f2 __attribute__((ext_vector_type(2)));
 
 template <int R0_, int R1_>
 struct WavePlan {
@@ -165,18 +163,13 @@ __device__ __forceinline__ h8 cmul_pack(f4 dr, f4 di, float4 w01, float4 w23) {
   return o;
 }
 
-// The same in packed fp16 (fp16 products): the accumulators rounded to fp16 once, w from
-// the fp16 table as [wr0 wr1 wr2 wr3 | wi0 wi1 wi2 wi3], two packed products per pair of
-// values.
+// The same as a product in packed fp16 (the fp16-accumulation mode, cmul_hp): the
+// accumulators rounded to fp16, w from the fp16 table as [wr0 wr1 wr2 wr3 | wi0 wi1 wi2 wi3].
 __device__ __forceinline__ h8 cmul_pack_h(f4 dr, f4 di, h8 w) {
-  const h2 r01 = __builtin_convertvector((f2){dr[0], dr[1]}, h2);
-  const h2 r23 = __builtin_convertvector((f2){dr[2], dr[3]}, h2);
-  const h2 i01 = __builtin_convertvector((f2){di[0], di[1]}, h2);
-  const h2 i23 = __builtin_convertvector((f2){di[2], di[3]}, h2);
-  const h2 wr01 = {w[0], w[1]}, wr23 = {w[2], w[3]}, wi01 = {w[4], w[5]}, wi23 = {w[6], w[7]};
-  const h2 or01 = r01 * wr01 - i01 * wi01, or23 = r23 * wr23 - i23 * wi23;
-  const h2 oi01 = r01 * wi01 + i01 * wr01, oi23 = r23 * wi23 + i23 * wr23;
-  return (h8){or01[0], or01[1], or23[0], or23[1], oi01[0], oi01[1], oi23[0], oi23[1]};
+  const HW hw{(h2){w[0], w[1]}, (h2){w[2], w[3]}, (h2){w[4], w[5]}, (h2){w[6], w[7]}};
+  h4 xr, xi;
+  cmul_hp(dr, di, hw, xr, xi);
+  return join_h8(xr, xi);
 }
 
 // conj((dr + i di) * k) for four spectrum values k (float4 pairs of complex64); with
@@ -199,6 +192,21 @@ __device__ __forceinline__ h8 spectrum_conj_pack(f4 dr, f4 di, float4 k01, float
   return o;
 }
 
+// spectrum_conj_pack, or with HP (the fp16-accumulation mode) the same product in packed
+// fp16 on the raw accumulators (cmul_hp, conjugated)
+template <bool CONJ, bool HP>
+__device__ __forceinline__ h8 spec_pack(f4 dr, f4 di, float4 k01, float4 k23) {
+  if constexpr (HP) {
+    const float kr[4] = {k01.x, k01.z, k23.x, k23.z};
+    const float ki[4] = {CONJ ? -k01.y : k01.y, CONJ ? -k01.w : k01.w, CONJ ? -k23.y : k23.y, CONJ ? -k23.w : k23.w};
+    h4 xr, xi;
+    cmul_hp<true>(dr, di, hw_of(kr, ki), xr, xi);
+    return join_h8(xr, xi);
+  } else {
+    return spectrum_conj_pack<CONJ>(dr, di, k01, k23);
+  }
+}
+
 // conj(D * K) for lane (j, g) of the phase-2 tile of strip s and k1 tile kt, from a
 // Hermitian half spectrum: K at k0 = 16s + j and k1 = 16kt + 4g + v, v = 0..3. Columns
 // k0 < R0/2 are read directly. A column k0 >= R0/2 holds conj(K) of the partner
@@ -206,25 +214,25 @@ __device__ __forceinline__ h8 spectrum_conj_pack(f4 dr, f4 di, float4 k01, float
 // MT-1-kt, lane group 3-g and the other float4 of its pair, in reverse value order.
 // For R0 >= 32 a strip is wholly direct or wholly partner (no per-lane choice); with
 // R0 = 16 the single strip splits at lane j = 8.
-template <class P>
+template <class P, bool HP = false>
 __device__ __forceinline__ h8 herm_spectrum_pack(f4 dr, f4 di, const float4* SP, int s, int kt, int lane) {
   constexpr int R0 = P::R0, MT = P::MT;
   const int j = lane & 15, g = lane >> 4;
   const int dk0 = 16 * s + j, pk0 = R0 - 16 * s - j;
   if (16 * s + 15 < R0 / 2) {
-    return spectrum_conj_pack<false>(dr, di, SP[hs_index<P>(dk0, kt, 0, g)], SP[hs_index<P>(dk0, kt, 1, g)]);
+    return spec_pack<false, HP>(dr, di, SP[hs_index<P>(dk0, kt, 0, g)], SP[hs_index<P>(dk0, kt, 1, g)]);
   } else if (16 * s >= R0 / 2) {
     // p0: conj(K) of v = 1, 0; p1: of v = 3, 2
     const float4 p0 = SP[hs_index<P>(pk0, MT - 1 - kt, 1, 3 - g)];
     const float4 p1 = SP[hs_index<P>(pk0, MT - 1 - kt, 0, 3 - g)];
-    return spectrum_conj_pack<true>(dr, di, make_float4(p0.z, p0.w, p0.x, p0.y), make_float4(p1.z, p1.w, p1.x, p1.y));
+    return spec_pack<true, HP>(dr, di, make_float4(p0.z, p0.w, p0.x, p0.y), make_float4(p1.z, p1.w, p1.x, p1.y));
   } else {
     const bool dir = dk0 < R0 / 2;
     const float4 a0 = SP[dir ? hs_index<P>(dk0, kt, 0, g) : hs_index<P>(pk0, MT - 1 - kt, 1, 3 - g)];
     const float4 a1 = SP[dir ? hs_index<P>(dk0, kt, 1, g) : hs_index<P>(pk0, MT - 1 - kt, 0, 3 - g)];
     const float4 k01 = dir ? a0 : make_float4(a0.z, -a0.w, a0.x, -a0.y);
     const float4 k23 = dir ? a1 : make_float4(a1.z, -a1.w, a1.x, -a1.y);
-    return spectrum_conj_pack<false>(dr, di, k01, k23);
+    return spec_pack<false, HP>(dr, di, k01, k23);
   }
 }
 
@@ -503,9 +511,10 @@ __device__ __forceinline__ void process_pair(const PairLoads<P, TIO>& d, TIO* S,
 #pragma unroll
       for (int j = 0; j < SG; j++) {
         const int s = s0 + j, tile = s * MT + kt;
-        const f4 r = acc_round<ACC16>(dr[j]), i = acc_round<ACC16>(di[j]);
+        // HP rounds the raw accumulators itself
+        const f4 r = HP ? dr[j] : acc_round<ACC16>(dr[j]), i = HP ? di[j] : acc_round<ACC16>(di[j]);
         if constexpr (HERM)
-          a2[j][kt] = herm_spectrum_pack<P>(r, i, SP, s, kt, lane);
+          a2[j][kt] = herm_spectrum_pack<P, HP>(r, i, SP, s, kt, lane);
         else
           a2[j][kt] = spectrum_conj_pack(r, i, SP[sp_index(tile, lane, 0)], SP[sp_index(tile, lane, 1)]);
       }
@@ -571,8 +580,8 @@ __global__ void __launch_bounds__(64 * NW)
     fftconv_wave_kernel(const TIO* __restrict__ u, const float4* __restrict__ kf, TIO* __restrict__ y, int B,
                         int H, const h8* __restrict__ ftab, const float4* __restrict__ twtab) {
   constexpr int R0 = P::R0;
-  // fp16 products: bf16 I/O and the fp16-accumulation mode (real filters)
-  constexpr bool HP = HERM && (sizeof(TIO) == 2 || ACC16);
+  // fp16 products: the fp16-accumulation mode (real filters)
+  constexpr bool HP = HERM && ACC16;
 #ifdef SFFFT_WAVE_FORCE_K1
   constexpr bool K1 = true;
 #else

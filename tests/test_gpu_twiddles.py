@@ -2,8 +2,8 @@
 w^e = exp(-2 pi i e / N) with e the product of an index and a frequency digit.
 
 - The wave pipeline's fp32 tables (built in fp64 on the host, read back through
-  sffft_twiddle_table), and their fp16 form for the fp16-products kernels (within half an
-  fp16 ulp). Every entry of TW1 = sc0 w^(m k0) and TW2 = sc0 sc1 w^(k0 n1) at its
+  sffft_twiddle_table), and their fp16 form for the fp16-accumulation kernels (within half
+  an fp16 ulp). Every entry of TW1 = sc0 w^(m k0) and TW2 = sc0 sc1 w^(k0 n1) at its
   slot of the documented layout (tile, lane (c, g), value v; m = 16 mt + 4 g + v,
   k0 = 16 nt + c for TW1, k0 = 16 s + 4 g + v, n1 = 16 t + c for TW2), against numpy's fp64
   cos/sin of the exact angle: within one fp32 rounding, |err| <= 2^-24 |w|.
@@ -118,8 +118,8 @@ def test_wave_twiddle_tables(r0, r1, split):
 
 @pytest.mark.parametrize("r0,r1", sorted({(r0, r1) for r0, r1, split in _table_plans() if split or r0 == r1 == 64}))
 def test_wave_twiddle_tables_fp16(r0, r1):
-    """The fp16 tables of the fp16-products wave kernels (bf16 I/O, fp16 accumulation): the
-    same values rounded to fp16, within half an fp16 ulp of the fp64 definition."""
+    """The fp16 tables of the fp16-accumulation wave kernels: the same values rounded to
+    fp16, within half an fp16 ulp of the fp64 definition."""
     N = r0 * r1
     raw = np.zeros(N * 4, np.float16)
     rc = sf.lib().sffft_twiddle_table(r0, r1, 2, raw.ctypes.data_as(ctypes.c_void_p), raw.nbytes)
