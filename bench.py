@@ -461,6 +461,14 @@ def sweep(a, sf, torch, np, dev, cover, clocks):
             step(0)
             torch.cuda.synchronize()
             err = oracle.rel_l2(sets[0]["y"].float().cpu().numpy(), ref)
+            # the same plan in the fp16-accumulation mode (its packed fp16 products), on the
+            # same buffers: the reference's speed-for-precision trade (README.md:112-122)
+            plan16 = plan.replace(acc=1)
+            t16 = time_fused(sf, torch, cover, sets, plan16, a.steps, 3, warm=False, gpu_warm_ms=a.gpu_warm_ms,
+                             repeats=a.repeats)
+            t16["step"](0)
+            torch.cuda.synchronize()
+            err16 = oracle.rel_l2(sets[0]["y"].float().cpu().numpy(), ref)
             if io == "fp32":
                 s0 = sets[0]
                 rp = sf.RocfftPipeline(B, H, L, s0["k"])
@@ -481,12 +489,17 @@ def sweep(a, sf, torch, np, dev, cover, clocks):
                    "rocfft_core_ms": None if rocfft_core_ms is None else round(rocfft_core_ms, 6),
                    "rocfft_rel_l2_vs_fp64": rocfft_err,
                    "speedup_vs_rocfft": None if rocfft_ms is None else round(rocfft_ms / ms_ref, 2),
-                   "graph_replay_bitexact": bool(exact), "rotated_sets": len(sets)}
+                   "graph_replay_bitexact": bool(exact), "rotated_sets": len(sets),
+                   "fp16acc": {"ms": round(t16["ms"], 6), "ms_min": round(t16["ms_min"], 6),
+                               "ms_max": round(t16["ms_max"], 6),
+                               "roofline_frac": round(algo / (t16["ms"] * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                               "rel_l2_vs_fp64": err16, "graph_replay_bitexact": bool(t16["exact"])}}
             if xcheck is not None:
                 row["oracle_fft_vs_direct"] = xcheck
             rows.append(row)
             print(f"# sweep L={L} {io} {plan.name()}: {ms * 1e3:.2f} us (min {t['ms_min'] * 1e3:.2f} max "
-                  f"{t['ms_max'] * 1e3:.2f}) frac {row['roofline_frac']} err {err:.3e} rocfft {rocfft_ms} "
+                  f"{t['ms_max'] * 1e3:.2f}) frac {row['roofline_frac']} err {err:.3e}; fp16 acc "
+                  f"{t16['ms'] * 1e3:.2f} us err {err16:.3e}; rocfft {rocfft_ms} "
                   f"clocks {clock_brief(t['clocks'])} ({time.perf_counter() - t0:.1f} s)", file=sys.stderr,
                   flush=True)
             del sets

@@ -1096,6 +1096,16 @@ __host__ __device__ constexpr int lds_waves_per_simd() {
   return (163840 / P::LDS_BYTES) * NW / 4 < 1 ? 1 : (163840 / P::LDS_BYTES) * NW / 4 > 8 ? 8 : (163840 / P::LDS_BYTES) * NW / 4;
 }
 
+// fp32 splits of a three-stage plan with fp32 I/O (bits as SFFFT_FP32_SPLITS). At N = 8192
+// (L = 4096) the pair plans measured 4.7e-4 (0.94 of the fp32 bound) with the input split
+// alone; the operand of the inverse stage over k1 also carrying its remainder (bit 2,
+// twice that stage's MFMAs) brings them to 4.4e-4 for 5-8% time. The other lengths stay
+// at or below 4.3e-4 without it.
+template <class P>
+constexpr int fp32_splits() {
+  return SFFFT_FP32_SPLITS | (P::S == 3 && P::N == 8192 ? 4 : 0);
+}
+
 // grid = H * (B / NSEQ) workgroups of 64*NW lanes; one sequence (NSEQ = 1) or one
 // pair of sequences of the same channel (NSEQ = 2) per workgroup.
 // ACC16 (fp16-accumulation mode) is a compile-time choice: as a runtime flag every
@@ -1137,7 +1147,7 @@ __global__ void __launch_bounds__(64 * NW, WPE)
   } else {
     phase1<P, NW, NSEQ, TIO, CACHED, SPLIT_IN>(ad, fr, re, im, ftab, acc16, lane, wave);
     __syncthreads();
-    phase2_s3<P, NW, CACHED, sizeof(TIO) == 4 && !ACC16 ? SFFFT_FP32_SPLITS : 0>(re, im, K, ftab, acc16, lane, wave);
+    phase2_s3<P, NW, CACHED, sizeof(TIO) == 4 && !ACC16 ? fp32_splits<P>() : 0>(re, im, K, ftab, acc16, lane, wave);
   }
   __syncthreads();
   phase3<P, NW, NSEQ, TIO, CACHED>(y + row_a, y + row_b, re, im, ftab, acc16, lane, wave);

@@ -698,6 +698,7 @@ __global__ void __launch_bounds__(64 * NW)
     // live (or spilled) across it
     int ln = lane;
     __asm__ volatile("" : "+v"(ln));
+    ln &= 63;  // known to be a lane index again: the row-chunk masks stay compile-time
     const int c = p / BP, bp = p - c * BP;
     const size_t ra = ((size_t)(2 * bp) * H + h0 + c) * P::L, rb = ra + (size_t)H * P::L;
     issue_pair_loads<P, TIO>(u + ra, u + rb, cur, ln);

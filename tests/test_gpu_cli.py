@@ -110,3 +110,19 @@ def test_full_size_rows_and_speedup(dev):
     sel = [r for r in rows if r[0] == "SELECT"][0]
     assert ref_err < 1e-6
     assert num(sel[5]) <= 5e-4 and pipe / num(sel[4]) >= 4.0, (pipe, sel)
+
+
+def test_fp16_accumulation_selected_where_it_wins(dev):
+    """fp16 accumulation is the reference's speed-for-precision trade (README.md:112-122):
+    here its products run in packed fp16, so at L = 1024 with bf16 I/O it is the fastest
+    candidate within a 3e-3 budget (about 10.5 against 12 us for fp32 accumulation) and the
+    selector takes it."""
+    rc, rows, _ = run(["8", "768", "1024", "--io", "bf16", "--kernel", "cached", "--max-error", "3e-3"])
+    assert rc == 0
+    sel = [r for r in rows if r[0] == "SELECT"]
+    fused = [r for r in rows if r[0] == "RESULT" and r[2].startswith("fused") and r[2].endswith("bf16io")]
+    for acc in ("fused_bf16io", "fused_fp16acc_bf16io"):
+        best = min((r for r in fused if r[2] == acc), key=lambda r: num(r[4]))
+        print(f"{acc}: {best[3]} {num(best[4]):.5f} ms err {num(best[5]):.3e}", flush=True)
+    assert len(sel) == 1 and sel[0][2] == "fused_fp16acc_bf16io", sel
+    assert num(sel[0][5]) <= 3e-3
