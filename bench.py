@@ -114,17 +114,22 @@ class Cover:
         torch.cuda.synchronize()
         self.cycles_per_ms = (1 << 22) / max(e0.elapsed_time(e1), 1e-3)
 
-    def __call__(self, ms: float) -> None:
-        self.torch.cuda._sleep(int(self.cycles_per_ms * ms))
+    def __call__(self, ms: float) -> int:
+        cycles = int(self.cycles_per_ms * ms)
+        self.torch.cuda._sleep(cycles)
+        return cycles
 
 
 class Clocks:
     """GFX clock (SCLK), memory clock (MCLK), socket power, hotspot temperature and GFX
-    activity of the GPU behind cuda:0, read through amdsmi (matched by PCI address), so that
-    timings taken on different boxes or at different points of one run can be told apart.
+    activity of the GPU behind cuda:0, read through amdsmi (matched by PCI address).
     start() begins sampling every couple of milliseconds on a host thread, stop() returns the
-    median, min and max of each field over the samples. Reading only; an "error" entry where
-    the library or the device is unavailable."""
+    median, min and max of each field over the samples and how many distinct readings there
+    were. On the boxes measured the metrics table refreshed far more slowly than the timed
+    regions last (one reading through a whole 300 ms window, idle values during load), so
+    the GFX clock of a timed region comes from its spin kernel instead (events_ms); these
+    readings describe the box, not the region. Reading only; an "error" entry where the
+    library or the device is unavailable."""
 
     FIELDS = (("sclk_mhz", ("current_gfxclk", "current_gfxclks", "average_gfxclk_frequency")),
               ("mclk_mhz", ("current_uclk", "average_uclk_frequency")),
@@ -204,7 +209,7 @@ class Clocks:
         self._thread.join()
         self._thread = None
         good = [x for x in self._samples if "error" not in x]
-        out = {"samples": len(good)}
+        out = {"samples": len(good), "distinct": len({tuple(sorted(x.items())) for x in good})}
         for key, _ in self.FIELDS:
             vals = [x[key] for x in good if x.get(key) is not None]
             out[key] = ({"median": statistics.median(vals), "min": min(vals), "max": max(vals)} if vals else None)
@@ -212,25 +217,34 @@ class Clocks:
 
 
 def clock_brief(c):
-    """Median SCLK/MCLK/power of a Clocks.stop() summary, for the progress lines."""
-    if not c or "error" in c:
-        return c
-    med = lambda k: None if c.get(k) is None else c[k]["median"]  # noqa: E731
-    return f"sclk {med('sclk_mhz')} MHz mclk {med('mclk_mhz')} MHz {med('power_w')} W ({c['samples']} samples)"
+    """The spin-measured GFX clock of the timed replays and the amdsmi power reading, for
+    the progress lines."""
+    import statistics
+
+    spin = c.get("sclk_mhz_spin") or []
+    a = c.get("amdsmi") or {}
+    pw = a.get("power_w") if isinstance(a, dict) else None
+    return (f"sclk {statistics.median(spin) if spin else None} MHz (spin), amdsmi "
+            f"{pw['median'] if isinstance(pw, dict) else None} W")
 
 
-def events_ms(cover, fn, reps, host_ms):
+def events_ms(cover, fn, reps, host_ms, sclk=None):
     """Average ms per rep of fn() between two events on the current stream, with the
-    spin kernel covering the host's enqueue time (host_ms, measured beforehand)."""
+    spin kernel covering the host's enqueue time (host_ms, measured beforehand). The spin
+    counts shader-clock cycles (s_memtime), so its own duration gives the GFX clock just
+    before the timed region: appended to `sclk` in MHz when a list is given."""
     import torch
 
     torch.cuda.synchronize()
-    cover(max(0.3, 3.0 * host_ms + 0.1))
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    es, e0, e1 = (torch.cuda.Event(enable_timing=True) for _ in range(3))
+    es.record()
+    cycles = cover(max(0.3, 3.0 * host_ms + 0.1))
     e0.record()
     fn()
     e1.record()
     torch.cuda.synchronize()
+    if sclk is not None:
+        sclk.append(round(cycles / es.elapsed_time(e0) / 1e3, 1))
     return e0.elapsed_time(e1) / reps
 
 
@@ -362,8 +376,10 @@ def time_fused(sf, torch, cover, sets, plan, steps, warmup, work=None, warm=True
         torch.cuda.synchronize()
     host = host_time_ms(graph.replay)
     exact = all(torch.equal(s["y"], y0) for s, y0 in zip(sets, y_eager))
-    runs = [events_ms(cover, graph.replay, steps, host) for _ in range(max(1, repeats))]
-    clk = clocks.stop() if clocks else None
+    sclk = []
+    runs = [events_ms(cover, graph.replay, steps, host, sclk) for _ in range(max(1, repeats))]
+    clk = clocks.stop() if clocks else {}
+    clk = {"sclk_mhz_spin": sclk, "amdsmi": clk}
     exact = exact and all(torch.equal(s["y"], y0) for s, y0 in zip(sets, y_eager))
     eager = lambda: [step(i) for i in range(steps)]  # noqa: E731
     ms_eager = events_ms(cover, eager, steps, host_time_ms(eager))
@@ -712,8 +728,10 @@ def main():
         "io_only_frac": round(B * H * L * 2 * s_io / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
         "timing": ("HIP graph of the K steps replayed between events behind a spin kernel that covers the "
                    "host enqueue, after W eager warmup steps and untimed replays for gpu_warm_ms; value: the median "
-                   "ms per step of `repeats` such replays (ms_min, ms_max, ms_runs); clocks: amdsmi samples every "
-                   "2 ms through the untimed and timed replays; ms_eager: the same steps launched one by one"),
+                   "ms per step of `repeats` such replays (ms_min, ms_max, ms_runs); clocks: the GFX clock before each "
+                   "timed replay from its spin kernel (shader-clock cycles over event time), and amdsmi readings "
+                   "sampled through the replays (a slowly refreshed table); ms_eager: the same steps launched one "
+                   "by one"),
         "gpu_warm_ms": a.gpu_warm_ms,
         "graph_replay_bitexact": bool(replay_exact),
         "rel_l2_vs_fp64": rel_err,

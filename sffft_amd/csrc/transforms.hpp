@@ -113,14 +113,11 @@ __device__ __forceinline__ int bitrev(int k) {
 
 // Frequency digit k of a non-last stage's line times w_Nj^(k * inner), rounded to
 // complex64 once; store(k, value) for k = 0 .. R-1. The twiddles are powers of
-// w_Nj^inner, built by recurrence in fp64 (same rounding rule as line_dft).
+// w_Nj^inner = w1c + i w1s, built by recurrence in fp64 (same rounding rule as line_dft).
 template <int R, class Store>
-__device__ __forceinline__ void twiddled_outputs(const double (&vr)[R], const double (&vi)[R], int inner, int Nj,
-                                                 int sign, Store store) {
+__device__ __forceinline__ void twiddled_outputs_w(const double (&vr)[R], const double (&vi)[R], double w1c,
+                                                   double w1s, Store store) {
 #pragma clang fp contract(off)
-  double w1s, w1c;
-  sincospi(2.0 * (double)inner / (double)Nj, &w1s, &w1c);
-  w1s *= sign;
   double wr = 1.0, wi = 0.0;
 #pragma unroll
   for (int k = 0; k < R; k++) {
@@ -130,6 +127,15 @@ __device__ __forceinline__ void twiddled_outputs(const double (&vr)[R], const do
     wi = fma(wr, w1s, wi * w1c);
     wr = nr;
   }
+}
+
+// The same with w_Nj^inner evaluated here (one fp64 sincospi of the exact angle).
+template <int R, class Store>
+__device__ __forceinline__ void twiddled_outputs(const double (&vr)[R], const double (&vi)[R], int inner, int Nj,
+                                                 int sign, Store store) {
+  double w1s, w1c;
+  sincospi(2.0 * (double)inner / (double)Nj, &w1s, &w1c);
+  twiddled_outputs_w<R>(vr, vi, w1c, sign * w1s, store);
 }
 
 template <int R>
@@ -219,14 +225,20 @@ struct LineGeom {
   // one thread per radix-16 line: 256 threads, 512 at N = 8192, 1024 at N = 16384
   static constexpr int THREADS = SLOTS / MAX_RADIX;
   static constexpr int LDS = SLOTS + SLOTS / 16;
+  // twiddle bases of the non-last stages: w_N^j for j < N / 16 (w_Nj^inner = w_N^(inner N/Nj))
+  static constexpr int TW = N / MAX_RADIX > 1 ? N / MAX_RADIX : 1;
   // radix of the stage whose remaining product of radices is REST (16s first)
   static constexpr int radix(int rest) { return rest > MAX_RADIX ? MAX_RADIX : rest; }
 };
 
 // One stage over the workgroup's lines: REST is the product of this and the later
 // radices (REST = N at the first stage), R this stage's radix, sJ = REST / R its stride.
+// tc, ts: the workgroup's table of w_N^j = tc[j] + i sign ts[j], j < N/16. A line's twiddle
+// base w_REST^inner is entry inner * N/REST: sincospi of 2j/N there and of 2 inner/REST in
+// the staged kernel are the same exact fp64 argument, so both paths get the same bits.
 template <int N, int REST>
-__device__ __forceinline__ void line_stage(float2* buf, const double* wc, const double* ws, int sign, float scale) {
+__device__ __forceinline__ void line_stage(float2* buf, const double* wc, const double* ws, const double* tc,
+                                           const double* ts, int sign, float scale) {
   constexpr int R = LineGeom<N>::radix(REST), sJ = REST / R, LPS = N / R;
   constexpr int LINES = LineGeom<N>::G * LPS;
   constexpr bool LAST = REST == R;
@@ -249,11 +261,12 @@ __device__ __forceinline__ void line_stage(float2* buf, const double* wc, const 
         buf[lpad(base + k)] = make_float2((float)(vr[r] * scale), (float)(vi[r] * scale));
       }
     } else {
-      twiddled_outputs<R>(vr, vi, inner, REST, sign, [&](int k, float2 v) { buf[lpad(base + k * sJ)] = v; });
+      const int j = inner * (N / REST);
+      twiddled_outputs_w<R>(vr, vi, tc[j], sign * ts[j], [&](int k, float2 v) { buf[lpad(base + k * sJ)] = v; });
     }
   }
   __syncthreads();
-  if constexpr (!LAST) line_stage<N, REST / R>(buf, wc, ws, sign, scale);
+  if constexpr (!LAST) line_stage<N, REST / R>(buf, wc, ws, tc, ts, sign, scale);
 }
 
 // Position in the line, after the last stage, of natural-order frequency f: the digits
@@ -280,11 +293,19 @@ __global__ void __launch_bounds__(LineGeom<N>::THREADS)
   typedef LineGeom<N> LG;
   __shared__ float2 buf[LG::LDS];
   __shared__ double wc[MAX_RADIX], ws[MAX_RADIX];
+  __shared__ double tc[LG::TW], ts[LG::TW];
   if (threadIdx.x < MAX_RADIX) {
     double sn, c;
     sincospi(2.0 * (double)threadIdx.x / (double)MAX_RADIX, &sn, &c);
     wc[threadIdx.x] = c;
     ws[threadIdx.x] = sign * sn;
+  }
+  // one sincospi per table entry instead of one per line and stage
+  for (int j = threadIdx.x; j < LG::TW; j += LG::THREADS) {
+    double sn, c;
+    sincospi(2.0 * (double)j / (double)N, &sn, &c);
+    tc[j] = c;
+    ts[j] = sn;
   }
   const long long s0 = (long long)blockIdx.x * LG::G;
   const int G = q.nseq - s0 < LG::G ? (int)(q.nseq - s0) : LG::G;
@@ -293,7 +314,7 @@ __global__ void __launch_bounds__(LineGeom<N>::THREADS)
     buf[lpad(i)] = g < G ? in[q.base(s0 + g) + (i - g * N)] : make_float2(0.f, 0.f);
   }
   __syncthreads();
-  line_stage<N, N>(buf, wc, ws, sign, scale);
+  line_stage<N, N>(buf, wc, ws, tc, ts, sign, scale);
   for (int i = threadIdx.x; i < G * N; i += LG::THREADS) {
     const int g = i / N, f = i - g * N;
     out[q.base(s0 + g) + f] = buf[lpad(g * N + line_position<N>(f))];

@@ -8,10 +8,12 @@ driver (`sffft`, the reference's CLI) on the reference's own input generator
   plan is a statistical quantity of the schedule, so a one-sequence plan must land within
   25% of the published value. A plan that packs two sequences into one transform carries
   about 1.2x the one-sequence noise (the imaginary half of each transform holds the second
-  sequence); the three-stage plans and the wave plans up to L = 512 feed the fp32 input as
-  an fp16 value plus its remainder, which removes one of their fp16 roundings. Every plan
-  is held to [0.75, 1.25] of the published value. bf16 I/O errors are dominated by the I/O
-  rounding and must land within 25% in every case.
+  sequence); the workgroup plans and the wave plans up to L = 512 feed the fp32 input as an
+  fp16 value plus its remainder, which removes one of their fp16 roundings (the reference
+  rounds it), so fp32-I/O errors may fall to 0.6 of the published value. Every fp32-I/O plan
+  is held to [0.6, 1.25] of it: a plan more than 25% less accurate than the reference
+  fails. bf16 I/O errors are dominated by the I/O rounding and must land within 25% in
+  every case.
 - the speed target of the fused kernel: the selected fused candidate at least 4x faster than
   the rocFFT pad/R2C/multiply/C2R/slice pipeline at every L of the reference's sweep
   (src/sffft.cu:372-381,506-513), for fp32 and bf16 I/O.
@@ -78,8 +80,9 @@ def test_per_plan_errors_match_the_published_values(dev):
             continue
         published = pub[0] if r[2] == "fused_fp32io" else pub[1]
         ratio = err / published
+        lo = 0.6 if r[2] == "fused_fp32io" else 0.75
         print(f"L={L} {r[2]} {cfg}: {err:.3e} / published {published:.3e} = {ratio:.3f}", flush=True)
-        assert 0.75 <= ratio <= 1.25, (L, r[2], cfg, err, pub)
+        assert lo <= ratio <= 1.25, (L, r[2], cfg, err, pub)
         checked += 1
     assert checked >= 2 * len(PUBLISHED) - 8, checked  # nearly every published plan is compiled here
 
