@@ -44,7 +44,7 @@ extern "C" {
  *           1 = one wavefront per transform, stages chained in registers, `waves`
  *               wavefronts per workgroup sharing LDS-resident DFT and twiddle tables
  *               (two-stage plans, seqs = 2; the first call for such a plan on a device
- *               uploads its immutable twiddle table, 16*L bytes)
+ *               uploads its immutable twiddle tables, 32*L bytes; 16*L for acc = 1)
  *   channels : mode 1 only: channels per workgroup; their spectra are copied into
  *           LDS once and shared by the wavefronts of each channel (mode 0: 1)
  *   mode 2 : multi-pass (sffft_conv_long_*): N = r0 * (r1 * r2), a column transform of

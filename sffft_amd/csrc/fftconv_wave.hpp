@@ -698,7 +698,10 @@ __global__ void __launch_bounds__(64 * NW)
     // live (or spilled) across it
     int ln = lane;
     __asm__ volatile("" : "+v"(ln));
-    ln &= 63;  // known to be a lane index again: the row-chunk masks stay compile-time
+    // 64x64 only: known to be a lane index again, its row-chunk masks fold (144 instead of
+    // 168 VGPRs in the fp16-accumulation instantiation). In the other plans the same mask
+    // raised the allocation, to a spill of 8-28 values at 64x32.
+    if constexpr (P::R0 == 64 && P::R1 == 64) ln &= 63;
     const int c = p / BP, bp = p - c * BP;
     const size_t ra = ((size_t)(2 * bp) * H + h0 + c) * P::L, rb = ra + (size_t)H * P::L;
     issue_pair_loads<P, TIO>(u + ra, u + rb, cur, ln);
