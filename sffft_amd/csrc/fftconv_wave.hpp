@@ -686,6 +686,18 @@ __global__ void __launch_bounds__(64 * NW)
   constexpr bool SPLIT = sizeof(TIO) == 4 && !ACC16 && P::L <= 512;
   if (wave < npairs) {
     const int c = wave / BP, bp = wave - c * BP;
+    // 64x64: a SIMD's three wavefronts hold one pair of each channel, whose data lands
+    // in channel order, and the last channel's compute sets the end of the launch. Its
+    // wavefronts issue first (priority rising with the channel); the earlier channels
+    // fill the issue slots it leaves. Alternating builds, two runs each, on two boxes:
+    // fp32 I/O 30.6-31.0 -> 29.3-29.4 us and 29.0-29.1 -> 28.7-28.9, bf16 25.1 -> 24.7-24.8
+    // and 24.0 -> 23.7-23.9, bf16 with fp16 accumulation 24.3 -> 23.2 and 23.4-23.7 ->
+    // 22.5-22.7 (outputs bit-identical). fp32 I/O with fp16 accumulation went 30.0 -> 33.0
+    // and keeps one level.
+    if constexpr (P::R0 == 64 && P::R1 == 64 && !(HP && sizeof(TIO) == 4)) {
+      if (c == 1) __builtin_amdgcn_s_setprio(1);
+      else if (c >= 2) __builtin_amdgcn_s_setprio(2);
+    }
     const size_t ra = ((size_t)(2 * bp) * H + h0 + c) * P::L, rb = ra + (size_t)H * P::L;
     process_pair<P, TIO, ACC16, HOLD, K1, HERM, SPLIT, HP>(cur, S, spec(c), y + ra, y + rb, F0, F1, TW1, TW2, lane);
   }
