@@ -69,6 +69,9 @@ def parse():
     ap.add_argument("--check", type=int, default=1, help="verify every output against the fp64 oracle")
     ap.add_argument("--work-mb", type=float, default=0.0,
                     help="multi-pass plans: workspace size in MB (0: the library's default chunking)")
+    ap.add_argument("--floor-shapes", type=int, default=0,
+                    help="1: instead of the convolution, time the body-less kernel over a set of launch shapes "
+                         "(the dispatch floor against grid, block and LDS size)")
     ap.add_argument("--copy-mb", type=float, default=0.0,
                     help="instead of the convolution, time a plain device-to-device copy of this many MB "
                          "(bandwidth reference and the calibration run for HBM byte counters)")
@@ -295,6 +298,39 @@ def copy_reference(a):
     gbs = 2 * n * 4 / (ms * 1e-3) / 1e9
     print(json.dumps({"copy_bytes_per_step": 2 * n * 4, "ms_per_step": ms, "GB/s": round(gbs, 1),
                       "frac_of_8TBps": round(gbs / HBM_PEAK_GBS, 4)}), flush=True)
+
+
+FLOOR_SHAPES = ((1, 64, 0), (256, 768, 129024), (256, 768, 0), (256, 256, 129024), (256, 256, 0),
+                (256, 1024, 0), (768, 256, 92160), (768, 256, 0), (3072, 256, 40960), (3072, 256, 0),
+                (6144, 128, 9216), (6144, 128, 0))
+
+
+def floor_shapes(a):
+    """The dispatch floor per launch shape (grid workgroups, block lanes, LDS bytes): K
+    launches of the body-less kernel captured as one HIP graph and replayed between events,
+    as the convolution is; median of `repeats` replays per shape. Separates what the launch
+    shape of a plan controls (workgroup count, size, LDS request) from the per-kernel cost."""
+    import statistics
+
+    import torch
+
+    import sffft_amd as sf
+
+    cover = Cover()
+    rows = []
+    for grid, block, lds in FLOOR_SHAPES:
+        sf.dispatch_floor_shape(grid, block, lds)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            for _ in range(a.steps):
+                sf.dispatch_floor_shape(grid, block, lds)
+        graph.replay()
+        host = host_time_ms(graph.replay)
+        runs = [events_ms(cover, graph.replay, a.steps, host) for _ in range(max(1, a.repeats))]
+        rows.append({"grid": grid, "block": block, "lds_bytes": lds, "us": round(statistics.median(runs) * 1e3, 3),
+                     "us_min": round(min(runs) * 1e3, 3)})
+        print(f"# floor grid {grid} block {block} lds {lds}: {rows[-1]['us']:.3f} us", file=sys.stderr, flush=True)
+    print(json.dumps({"dispatch_floor_shapes": rows, "steps": a.steps, "repeats": a.repeats}), flush=True)
 
 
 def sinusoid_filters(torch, dev, H, L, g):
@@ -588,6 +624,9 @@ def main():
         sys.exit(2)
     if a.copy_mb > 0:
         copy_reference(a)
+        return
+    if a.floor_shapes:
+        floor_shapes(a)
         return
     import numpy as np
     import torch

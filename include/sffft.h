@@ -231,6 +231,12 @@ int sffft_to_bf16(const float* x, uint16_t* y, size_t n, void* stream);
    argument checks and error codes as sffft_conv_*, without the buffers. */
 int sffft_dispatch_floor(int B, int H, int L, const sffft_plan* plan, void* stream);
 
+/* The same body-less kernel with an explicit launch shape: grid workgroups of block lanes
+   (a multiple of 64, at most 1024) requesting lds_bytes of LDS (at most 163840), to
+   measure which part of the dispatch floor a launch shape controls. No counterpart in
+   the reference (a measurement aid). SFFFT_EINVAL for a shape outside those limits. */
+int sffft_dispatch_floor_shape(unsigned grid, unsigned block, unsigned lds_bytes, void* stream);
+
 /* Copies the device DFT coefficient table (57,344 bytes) to host memory `out`
  * (for tests). Returns SFFFT_EINVAL if out_len is too small. */
 int sffft_dft_table(void* out, size_t out_len);

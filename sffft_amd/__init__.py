@@ -133,6 +133,7 @@ def load_library(path: str) -> ctypes.CDLL:
         "sffft_circconv2d_f32": (ci, [vp, vp, vp, vp, sz, ci, ci, ci, ci, vp]),
         "sffft_to_bf16": (ci, [vp, vp, sz, vp]),
         "sffft_dispatch_floor": (ci, [ci, ci, ci, P, vp]),
+        "sffft_dispatch_floor_shape": (ci, [ctypes.c_uint, ctypes.c_uint, ctypes.c_uint, vp]),
         "sffft_dft_table": (ci, [vp, sz]),
         "sffft_twiddle_probe": (ci, [ci, vp, ci, ci, ctypes.c_float, vp, vp]),
         "sffft_twiddle_table": (ci, [ci, ci, ci, vp, sz]),
@@ -509,6 +510,11 @@ def to_bf16(x):
 def dispatch_floor(B: int, H: int, L: int, plan: Plan) -> None:
     """Launches the body-less kernel with the launch shape of conv() for this plan."""
     _check(lib().sffft_dispatch_floor(B, H, L, ctypes.byref(plan), _stream()), "sffft_dispatch_floor")
+
+
+def dispatch_floor_shape(grid: int, block: int, lds_bytes: int) -> None:
+    """The body-less kernel with an explicit launch shape (sffft_dispatch_floor_shape)."""
+    _check(lib().sffft_dispatch_floor_shape(grid, block, lds_bytes, _stream()), "sffft_dispatch_floor_shape")
 
 
 def dft_table():

@@ -767,6 +767,11 @@ int sffft_dispatch_floor(int B, int H, int L, const sffft_plan* plan, void* stre
   if (!e) return SFFFT_ENOPLAN;
   const unsigned grid = e->mode == 1 ? (unsigned)((H + e->channels - 1) / e->channels)
                                      : (unsigned)(H * (B / plan->seqs));
+  return sffft_dispatch_floor_shape(grid, 64u * (unsigned)plan->waves, (unsigned)e->lds_bytes, stream);
+}
+
+int sffft_dispatch_floor_shape(unsigned grid, unsigned block, unsigned lds_bytes, void* stream) {
+  if (grid < 1 || block < 64 || block > 1024 || block % 64 || lds_bytes > 163840) return SFFFT_EINVAL;
   static std::once_flag attr_once;
   static int attr_rc = SFFFT_OK;
   std::call_once(attr_once, [] {
@@ -775,8 +780,7 @@ int sffft_dispatch_floor(int B, int H, int L, const sffft_plan* plan, void* stre
                          "hipFuncSetAttribute");
   });
   if (attr_rc) return attr_rc;
-  hipLaunchKernelGGL(empty_dispatch_kernel, dim3(grid), dim3(64 * plan->waves), (unsigned)e->lds_bytes,
-                     (hipStream_t)stream);
+  hipLaunchKernelGGL(empty_dispatch_kernel, dim3(grid), dim3(block), lds_bytes, (hipStream_t)stream);
   return hip_status(hipGetLastError(), "dispatch floor launch");
 }
 

@@ -88,6 +88,8 @@ def test_conv_argument_errors_need_no_gpu():
     assert lib.sffft_dispatch_floor(0, 768, 1024, ctypes.byref(p), null) == sf.SFFFT_EINVAL
     assert lib.sffft_dispatch_floor(7, 768, 1024, ctypes.byref(p), null) == sf.SFFFT_EINVAL  # B odd
     assert lib.sffft_dispatch_floor(8, 768, 1000, ctypes.byref(p), null) == sf.SFFFT_EINVAL  # L
+    for shape in ((0, 256, 0), (256, 0, 0), (256, 96, 0), (256, 1088, 0), (256, 256, 163841)):
+        assert lib.sffft_dispatch_floor_shape(*shape, null) == sf.SFFFT_EINVAL, shape
 
 
 def test_strerror():
