@@ -693,8 +693,11 @@ __global__ void __launch_bounds__(64 * NW)
     // fp32 I/O 30.6-31.0 -> 29.3-29.4 us and 29.0-29.1 -> 28.7-28.9, bf16 25.1 -> 24.7-24.8
     // and 24.0 -> 23.7-23.9, bf16 with fp16 accumulation 24.3 -> 23.2 and 23.4-23.7 ->
     // 22.5-22.7 (outputs bit-identical). fp32 I/O with fp16 accumulation went 30.0 -> 33.0
-    // and keeps one level.
-    if constexpr (P::R0 == 64 && P::R1 == 64 && !(HP && sizeof(TIO) == 4)) {
+    // and keeps one level. 64x32 (L = 1024), three runs each: bf16 with fp16 accumulation
+    // 10.83-10.95 -> 10.32-10.58 us; bf16 unchanged (11.95-12.08 against 11.96-11.98) and
+    // fp32 with fp16 accumulation 5% slower, so only the first takes it.
+    if constexpr ((P::R0 == 64 && P::R1 == 64 && !(HP && sizeof(TIO) == 4)) ||
+                  (P::R0 == 64 && P::R1 == 32 && HP && sizeof(TIO) == 2)) {
       if (c == 1) __builtin_amdgcn_s_setprio(1);
       else if (c >= 2) __builtin_amdgcn_s_setprio(2);
     }
