@@ -17,11 +17,11 @@ import sffft_amd as sf
 BUILD = os.path.join(os.path.dirname(sf.LIB_PATH), "_build")
 
 
-def reports():
-    """{mangled kernel name: {field: value}} over every length's report (a field's bracketed
-    unit, as in `ScratchSize [bytes/lane]`, is dropped from its name)."""
+def reports(build=BUILD):
+    """{mangled kernel name: {field: value}} over every length's report in `build` (a
+    field's bracketed unit, as in `ScratchSize [bytes/lane]`, is dropped from its name)."""
     out = {}
-    for path in sorted(glob.glob(os.path.join(BUILD, "conv_L*.o.resources"))):
+    for path in sorted(glob.glob(os.path.join(build, "conv_L*.o.resources"))):
         cur = None
         for line in open(path):
             m = re.search(r"remark: Function Name: (\S+)", line)
@@ -77,13 +77,7 @@ def test_report_parser_reads_a_spill():
             "csrc/fftconv_wave.hpp:581:1: remark:     VGPRs Spill: 24 [-Rpass-analysis=kernel-resource-usage]\n")
     import tempfile
 
-    global BUILD
-    saved = BUILD
     with tempfile.TemporaryDirectory() as d:
         open(os.path.join(d, "conv_L1.o.resources"), "w").write(text)
-        BUILD = d
-        try:
-            r = reports()
-        finally:
-            BUILD = saved
+        r = reports(d)
     assert r == {"_ZN5sffft19k": {"VGPRs": "168", "ScratchSize": "100", "VGPRs Spill": "24"}}
