@@ -553,7 +553,7 @@ int permute_launch(const float2* src, float2* kf, int H, const sffft_plan* plan,
 // spectrum the correlations of the backward passes run on). The padded rows are transformed
 // in place in `work` (H * N complex64; fp64 stages, complex64 between them), then gathered
 // into kernel order. Up to 16384 points the transform is one pass through LDS and needs no
-// workspace. Longer rows take the staged transform, whose workspace is this call's own rows
+// workspace. Longer rows take the two-pass transform, whose workspace is this call's own rows
 // of kf: the gather overwrites them afterwards, and the results of earlier calls (the rows
 // of the channels before h0) lie before them.
 int spectrum_impl(const float* kr, const float* ki, int H, int L, int klen, const sffft_plan* plan, void* kf,

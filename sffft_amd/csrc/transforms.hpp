@@ -236,13 +236,14 @@ struct LineGeom {
 // tc, ts: the workgroup's table of w_N^j = tc[j] + i sign ts[j], j < N/16. A line's twiddle
 // base w_REST^inner is entry inner * N/REST: sincospi of 2j/N there and of 2 inner/REST in
 // the staged kernel are the same exact fp64 argument, so both paths get the same bits.
-template <int N, int REST>
+// G sequences of N in buf, THREADS threads (the one-pass kernel's geometry by default).
+template <int N, int REST, int G = LineGeom<N>::G, int THREADS = LineGeom<N>::THREADS>
 __device__ __forceinline__ void line_stage(float2* buf, const double* wc, const double* ws, const double* tc,
                                            const double* ts, int sign, float scale) {
   constexpr int R = LineGeom<N>::radix(REST), sJ = REST / R, LPS = N / R;
-  constexpr int LINES = LineGeom<N>::G * LPS;
+  constexpr int LINES = G * LPS;
   constexpr bool LAST = REST == R;
-  for (int li = threadIdx.x; li < LINES; li += LineGeom<N>::THREADS) {
+  for (int li = threadIdx.x; li < LINES; li += THREADS) {
     const int g = li / LPS, l = li - g * LPS;
     const int inner = l % sJ, base = g * N + (l / sJ) * REST + inner;
     double vr[R], vi[R];
@@ -266,7 +267,7 @@ __device__ __forceinline__ void line_stage(float2* buf, const double* wc, const 
     }
   }
   __syncthreads();
-  if constexpr (!LAST) line_stage<N, REST / R>(buf, wc, ws, tc, ts, sign, scale);
+  if constexpr (!LAST) line_stage<N, REST / R, G, THREADS>(buf, wc, ws, tc, ts, sign, scale);
 }
 
 // Position in the line, after the last stage, of natural-order frequency f: the digits
@@ -348,6 +349,194 @@ inline bool run_lines(const float2* in, float2* out, const Seqs& q, int N, int s
   }
 }
 
+// ---- two passes over long contiguous lines ------------------------------------------
+// Sequences of ONEPASS_MAX_N < N <= MAX_N points at unit stride: N = N1 * N2 with N1 = 16^k.
+// The first k stages move positions only within the N1-point columns p = c + m N2 (c < N2),
+// and leave N1 independent blocks of N2 contiguous positions, each of which the remaining
+// stages transform as an N2-point sequence (the same twiddles, w_Nj with Nj <= N2). So:
+//   pass A (col_kernel): C columns per workgroup, loaded as runs of C points from each of
+//   the N1 rows, stages 0..k-1 in LDS with the stage kernel's line DFTs and twiddles (the
+//   global inner index c + u N2), written back in place to the workspace;
+//   pass B (row_kernel): G blocks per workgroup, the one-pass stages of an N2-point
+//   sequence, and block b's frequency f written to k = rev(b) + N1 f, rev reversing b's k
+//   base-16 digits; the G blocks have consecutive rev(b), so the writes are runs of G points.
+// Each sequence crosses HBM twice each way instead of once per stage, with the staged
+// kernels' arithmetic in the same order: the results are bit-identical to them.
+constexpr int TWOPASS_MAX_N1 = 4096, TWOPASS_MAX_N2 = 4096;
+
+template <int N1>
+struct ColGeom {
+  static constexpr int C = N1 >= 1024 ? 4 : 4096 / N1;  // columns per workgroup
+  static constexpr int SLOTS = N1 * C;
+  static constexpr int THREADS = SLOTS / MAX_RADIX;
+};
+
+template <int N2>
+struct RowGeom {
+  static constexpr int G = N2 >= 1024 ? 4 : 4096 / N2;  // blocks per workgroup
+  static constexpr int SLOTS = G * N2;
+  static constexpr int THREADS = SLOTS / MAX_RADIX;
+  static constexpr int LDS = SLOTS + SLOTS / 16;
+};
+
+// stage of pass A whose local stride is LS (N1/16 at the first stage, 1 at the last)
+template <int N1, int LS>
+__device__ __forceinline__ void col_stage(float2* buf, const double* wc, const double* ws, int c0, int N2,
+                                          int sign) {
+  constexpr int R = MAX_RADIX, C = ColGeom<N1>::C, LINES = (N1 / R) * C;
+  for (int li = threadIdx.x; li < LINES; li += ColGeom<N1>::THREADS) {
+    const int j = li % C, l = li / C;  // column j (consecutive across threads), line l of it
+    const int lu = l % LS, mb = (l / LS) * R * LS + lu;
+    double vr[R], vi[R];
+#pragma unroll
+    for (int t = 0; t < R; t++) {
+      const float2 x = buf[(mb + t * LS) * C + j];
+      vr[t] = (double)x.x;
+      vi[t] = (double)x.y;
+    }
+    line_dft<R, R>(vr, vi, wc, ws);
+    // the stage kernel's twiddle of this line: inner = p mod sJ, Nj = R sJ, sJ = LS N2
+    twiddled_outputs<R>(vr, vi, c0 + j + lu * N2, R * LS * N2, sign,
+                        [&](int k, float2 v) { buf[(mb + k * LS) * C + j] = v; });
+  }
+  __syncthreads();
+  if constexpr (LS > 1) col_stage<N1, LS / R>(buf, wc, ws, c0, N2, sign);
+}
+
+template <int N1>
+__global__ void __launch_bounds__(ColGeom<N1>::THREADS)
+    col_kernel(const float2* in, float2* work, Seqs q, int N2, int sign) {
+  typedef ColGeom<N1> CG;
+  __shared__ float2 buf[CG::SLOTS];
+  __shared__ double wc[MAX_RADIX], ws[MAX_RADIX];
+  if (threadIdx.x < MAX_RADIX) {
+    double sn, c;
+    sincospi(2.0 * (double)threadIdx.x / (double)MAX_RADIX, &sn, &c);
+    wc[threadIdx.x] = c;
+    ws[threadIdx.x] = sign * sn;
+  }
+  const int per_seq = N2 / CG::C;
+  const long long s = blockIdx.x / per_seq;
+  const int c0 = (int)(blockIdx.x - s * per_seq) * CG::C;
+  const long long N = (long long)N1 * N2;
+  const float2* src = in + q.base(s) + c0;
+  for (int i = threadIdx.x; i < CG::SLOTS; i += CG::THREADS) {
+    const int m = i / CG::C, j = i - m * CG::C;
+    buf[i] = src[(long long)m * N2 + j];
+  }
+  __syncthreads();
+  col_stage<N1, N1 / MAX_RADIX>(buf, wc, ws, c0, N2, sign);
+  float2* dst = work + s * N + c0;
+  for (int i = threadIdx.x; i < CG::SLOTS; i += CG::THREADS) {
+    const int m = i / CG::C, j = i - m * CG::C;
+    dst[(long long)m * N2 + j] = buf[i];
+  }
+}
+
+// b's k base-16 digits reversed (an involution)
+__device__ __forceinline__ int digit_reverse16(int b, int k) {
+  int r = 0;
+  for (int i = 0; i < k; i++) {
+    r = (r << 4) | (b & 15);
+    b >>= 4;
+  }
+  return r;
+}
+
+template <int N2>
+__global__ void __launch_bounds__(RowGeom<N2>::THREADS)
+    row_kernel(const float2* work, float2* out, Seqs q, int N1, int k, int sign, float scale) {
+  typedef RowGeom<N2> RG;
+  typedef LineGeom<N2> LG;
+  __shared__ float2 buf[RG::LDS];
+  __shared__ double wc[MAX_RADIX], ws[MAX_RADIX];
+  __shared__ double tc[LG::TW], ts[LG::TW];
+  if (threadIdx.x < MAX_RADIX) {
+    double sn, c;
+    sincospi(2.0 * (double)threadIdx.x / (double)MAX_RADIX, &sn, &c);
+    wc[threadIdx.x] = c;
+    ws[threadIdx.x] = sign * sn;
+  }
+  for (int j = threadIdx.x; j < LG::TW; j += RG::THREADS) {
+    double sn, c;
+    sincospi(2.0 * (double)j / (double)N2, &sn, &c);
+    tc[j] = c;
+    ts[j] = sn;
+  }
+  const int per_seq = N1 / RG::G;
+  const long long s = blockIdx.x / per_seq;
+  const int r0 = (int)(blockIdx.x - s * per_seq) * RG::G;  // rev(b) of the first block
+  const long long N = (long long)N1 * N2;
+  const float2* src = work + s * N;
+  for (int i = threadIdx.x; i < RG::SLOTS; i += RG::THREADS) {
+    const int g = i / N2, e = i - g * N2;
+    buf[lpad(i)] = src[(long long)digit_reverse16(r0 + g, k) * N2 + e];
+  }
+  __syncthreads();
+  line_stage<N2, N2, RG::G, RG::THREADS>(buf, wc, ws, tc, ts, sign, scale);
+  float2* dst = out + q.base(s) + r0;
+  for (int i = threadIdx.x; i < RG::SLOTS; i += RG::THREADS) {
+    const int f = i / RG::G, g = i - f * RG::G;
+    dst[(long long)f * N1 + g] = buf[lpad(g * N2 + line_position<N2>(f))];
+  }
+}
+
+template <int N1>
+inline void launch_cols(const float2* in, float2* work, const Seqs& q, int N2, int sign, hipStream_t st) {
+  const unsigned grid = (unsigned)(q.nseq * (N2 / ColGeom<N1>::C));
+  hipLaunchKernelGGL(col_kernel<N1>, dim3(grid), dim3(ColGeom<N1>::THREADS), 0, st, in, work, q, N2, sign);
+}
+
+template <int N2>
+inline void launch_rows(const float2* work, float2* out, const Seqs& q, int N1, int k, int sign, float scale,
+                        hipStream_t st) {
+  const unsigned grid = (unsigned)(q.nseq * (N1 / RowGeom<N2>::G));
+  hipLaunchKernelGGL(row_kernel<N2>, dim3(grid), dim3(RowGeom<N2>::THREADS), 0, st, work, out, q, N1, k, sign,
+                     scale);
+}
+
+// The column count k (N1 = 16^k) whose passes read and write the longest runs: pass A's
+// runs are C points, pass B's G points; both passes within TWOPASS_MAX_N1 / _N2. 0 if none.
+inline int two_pass_k(long long N) {
+  int best = 0, best_run = 0;
+  for (int k = 1; k <= 3; k++) {
+    const long long N1 = 1LL << (4 * k), N2 = N / N1;
+    if (N1 > TWOPASS_MAX_N1 || N2 > TWOPASS_MAX_N2 || N2 < 16 || N1 * N2 != N) continue;
+    const int C = N1 >= 1024 ? 4 : (int)(4096 / N1), G = N2 >= 1024 ? 4 : (int)(4096 / N2);
+    if (G > N1 || C > N2) continue;
+    const int run = C < G ? C : G;
+    if (run > best_run) best = k, best_run = run;
+  }
+  return best;
+}
+
+inline bool run_two_pass(const float2* in, float2* out, float2* work, const Seqs& q, long long N, int sign,
+                         float scale, hipStream_t st) {
+  if (q.stride != 1 || q.seq_fast || N <= ONEPASS_MAX_N) return false;
+  const int k = two_pass_k(N);
+  if (!k) return false;
+  const int N1 = 1 << (4 * k), N2 = (int)(N / N1);
+  switch (N1) {
+    case 16: launch_cols<16>(in, work, q, N2, sign, st); break;
+    case 256: launch_cols<256>(in, work, q, N2, sign, st); break;
+    case 4096: launch_cols<4096>(in, work, q, N2, sign, st); break;
+    default: return false;
+  }
+  switch (N2) {
+    case 16: launch_rows<16>(work, out, q, N1, k, sign, scale, st); break;
+    case 32: launch_rows<32>(work, out, q, N1, k, sign, scale, st); break;
+    case 64: launch_rows<64>(work, out, q, N1, k, sign, scale, st); break;
+    case 128: launch_rows<128>(work, out, q, N1, k, sign, scale, st); break;
+    case 256: launch_rows<256>(work, out, q, N1, k, sign, scale, st); break;
+    case 512: launch_rows<512>(work, out, q, N1, k, sign, scale, st); break;
+    case 1024: launch_rows<1024>(work, out, q, N1, k, sign, scale, st); break;
+    case 2048: launch_rows<2048>(work, out, q, N1, k, sign, scale, st); break;
+    case 4096: launch_rows<4096>(work, out, q, N1, k, sign, scale, st); break;
+    default: return false;
+  }
+  return true;
+}
+
 // Workspace of one transform call: the stage results between the first and last stage.
 inline long long work_elems(const Seqs& q, long long N) {
   Radices d;
@@ -363,6 +552,7 @@ inline hipError_t run(const float2* in, float2* out, float2* work, const Seqs& q
   if (!split(N, &d)) return hipErrorInvalidValue;
   const int sign = inverse ? 1 : -1;
   if (N <= ONEPASS_MAX_N && run_lines(in, out, q, N, sign, scale, st)) return hipGetLastError();
+  if (run_two_pass(in, out, work, q, N, sign, scale, st)) return hipGetLastError();
   for (int J = 0; J < d.S; J++) {
     const long long threads = q.nseq * (N / d.r[J]);
     const dim3 grid((unsigned)((threads + 127) / 128)), block(128);

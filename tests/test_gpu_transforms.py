@@ -76,6 +76,23 @@ def test_one_pass_matches_staged_path_bitwise(batch, N):
         assert np.array_equal(a.view(np.uint32), b.view(np.uint32)), (N, inverse)
 
 
+@pytest.mark.parametrize("batch,N", [(2, 1 << 15), (3, 1 << 16), (2, 1 << 17), (2, 1 << 19), (2, 1 << 20),
+                                     (2, 1 << 21), (2, 1 << 24)])
+def test_two_pass_matches_staged_path_bitwise(batch, N):
+    """Contiguous sequences of 16384 < N <= 2^24 take the two-pass kernels (the first stages
+    on N1-point columns, then N2-point blocks, written in natural order); the same values as
+    the columns of a matrix take one launch per stage. Same arithmetic in the same order:
+    bit-identical, forward and inverse with a scale."""
+    print(f"two-pass vs staged batch={batch} N={N}", flush=True)
+    x = crandn(np.random.default_rng(N + 7 * batch), batch, N)
+    rows = torch.from_numpy(x).to(DEV)
+    cols = torch.from_numpy(np.ascontiguousarray(x.T)).to(DEV)
+    for inverse, scale in ((False, 1.0), (True, 1.0 / N)):
+        a = sf.fft(rows, inverse=inverse, scale=scale).cpu().numpy()
+        b = np.ascontiguousarray(sf.fft(cols, inverse=inverse, scale=scale, dim=0).cpu().numpy().T)
+        assert np.array_equal(a.view(np.uint32), b.view(np.uint32)), (N, inverse)
+
+
 @pytest.mark.parametrize("batch,N,stride,dist", [(3, 128, 2, 256), (3, 128, 3, 1), (2, 4096, 3, 12288),
                                                   (4, 256, 4, 1)])
 def test_fft_layout_family_edges(batch, N, stride, dist):
@@ -109,7 +126,7 @@ def test_spectrum_matches_fp64_dft(L):
     """sffft_spectrum against the same kernel-order gather (sffft_spectrum_from_natural)
     applied to numpy's fp64 DFT of the zero-padded filters, rounded to complex64, for every
     compiled plan. Up to N = 16384 the spectrum runs the one-pass transform above, beyond it
-    the staged transform with the spectrum's own rows as workspace (L = 16384: workgroup
+    the two-pass transform with the spectrum's own rows as workspace (L = 16384: workgroup
     plans; L = 32768: multi-pass plans)."""
     print(f"spectrum L={L}", flush=True)
     H = 7
